@@ -1,0 +1,179 @@
+/*
+ * madi_q8.h -- C ABI of the MI355X (gfx950) Q8 matmul path.
+ *
+ * Drop-in for the Whisper large-v3-turbo engine's Q8 matmul operators.  The
+ * engine's Zig operator wrappers keep their signatures and lower to these
+ * entry points instead of the Metal bridge (engine/metal/metal_backend.h).
+ * Every entry point takes plain pointers and sizes, returns 0 on success or a
+ * negative MADI_ERR_* code, and records a message for madi_last_error().
+ *
+ * Memory: madi_alloc returns DEVICE memory (HBM).  Unlike Metal's unified
+ * buffers it is not host-addressable: the host fills it with madi_upload and
+ * reads it with madi_download.  All op pointers are device pointers.
+ *
+ * Ordering: every op is enqueued on one HIP stream (the null stream unless
+ * madi_set_stream chose another) and runs in call order; nothing blocks until
+ * madi_sync.  Like the Metal bridge, the library keeps one global queue and
+ * expects calls from one host thread at a time.
+ *
+ * ---------------------------------------------------------------------------
+ * Q8 weights.  A Q8_0 weight W[N][K] (K % 32 == 0) is int8 quants plus one
+ * fp16 scale per 32-element K block: w[n][k] = q[n][k] * s[n][k/32]
+ * (engine/metal/encoder.zig:21, decoder.zig:22).  The reference stores them
+ * row-major ("natural": qs[n*K+k], scales[n*(K/32)+k/32]).
+ *
+ * The loader repacks them once (madi_q8_repack / madi_q8_repack_host) into
+ * the CDNA4 PANEL layout that every op below reads.  Requires K % 64 == 0.
+ *   panel p      = rows [32p, 32p+R), R = min(32, N-32p)
+ *   qs   bytes   : panel p starts at byte 32*p*K (same offset as natural), then
+ *                  chunk c (k in [64c, 64c+64)) at c*R*64, then the 16-byte
+ *                  unit (j, h, r) at ((2j+h)*R + r)*16 holding
+ *                  q[32p+r][64c+32h+16j+i] + 128 (uint8), i = 0..15
+ *   scales fp16  : panel p starts at element 32*p*(K/32) (same offset as
+ *                  natural), chunk c at c*2R, element (h, r) at h*R + r holding
+ *                  s[32p+r][2c+h]
+ * Buffer sizes are unchanged (N*K bytes, N*K/32 scales) and every panel keeps
+ * its natural offset, so the engine's row slicing of stacked weights
+ * (qs + D*D, scales + D*(D/32); engine/metal/encoder.zig:263-267) stays valid
+ * at any row offset that is a multiple of 32.  For a full panel the 1 KiB
+ * half-chunk j is exactly one wave64 load of 16 bytes per lane, lane = 32h+r,
+ * and lane (h, r) holds the 32 weights of ONE quantisation block.
+ * ---------------------------------------------------------------------------
+ */
+#ifndef MADI_Q8_H
+#define MADI_Q8_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Return codes.  The reference bridge returns 0 / -1 (metal_backend.h:14-46)
+ * and the Zig wrapper maps failures to error{InitFailed, LibraryLoadFailed,
+ * FunctionNotFound, AllocFailed, DispatchFailed, SyncFailed}
+ * (engine/metal/metal_backend.zig:34-41); the codes below refine -1. */
+#define MADI_OK 0
+#define MADI_ERR_INIT (-1)      /* InitFailed: no gfx950 device / HIP init error   */
+#define MADI_ERR_ALLOC (-2)     /* AllocFailed                                      */
+#define MADI_ERR_DISPATCH (-3)  /* DispatchFailed: kernel launch failed             */
+#define MADI_ERR_SYNC (-4)      /* SyncFailed: stream sync reported an error        */
+#define MADI_ERR_SHAPE (-5)     /* unsupported shape (K % 64, zero sizes, ...)      */
+#define MADI_ERR_NULL (-6)      /* required pointer is NULL                         */
+#define MADI_ERR_ALIGN (-7)     /* pointer not aligned as the op requires           */
+#define MADI_ERR_NOT_INIT (-8)  /* madi_init has not succeeded                      */
+#define MADI_ERR_ARG (-9)       /* bad enum / argument value                        */
+
+/* Epilogues of the fused GEMM / GEMV ops. */
+#define MADI_EPI_NONE 0      /* out = acc                                          */
+#define MADI_EPI_BIAS 1      /* out = acc + bias[n]                                */
+#define MADI_EPI_BIAS_GELU 2 /* out = gelu_erf(acc + bias[n])                      */
+#define MADI_EPI_BIAS_RES 3  /* out[n] = out[n] + acc + bias[n]  (GEMV only)       */
+
+/* ---- runtime ------------------------------------------------------------ */
+/* replaces mtl_init (metal_backend.h:15): selects device 0, checks gfx950. */
+int madi_init(void);
+/* replaces mtl_cleanup (metal_backend.h:16). */
+void madi_cleanup(void);
+/* replaces mtl_alloc (metal_backend.h:21): device memory, 256-byte aligned,
+ * NULL on failure. */
+void *madi_alloc(size_t size);
+/* replaces mtl_free (metal_backend.h:22). */
+void madi_free(void *ptr);
+/* replace mtl_upload / mtl_download (metal_backend.h:29-30): blocking copies
+ * host <-> device, ordered after previously enqueued ops. */
+int madi_upload(void *dst_device, const void *src_host, size_t size);
+int madi_download(void *dst_host, const void *src_device, size_t size);
+/* replace mtl_begin_command_buffer / mtl_commit_command_buffer / mtl_sync
+ * (metal_backend.h:62-69).  HIP launches are already queued asynchronously, so
+ * begin and commit only check state; sync waits for the stream. */
+int madi_begin_command_buffer(void);
+int madi_commit_command_buffer(void);
+int madi_sync(void);
+/* No reference counterpart: lets a host that owns a HIP stream (hipStream_t
+ * passed as void*) order this library's launches on it.  NULL = null stream. */
+int madi_set_stream(void *hip_stream);
+/* Message of the last failure on the calling thread ("" if none). */
+const char *madi_last_error(void);
+/* Number of compute units of the current device (0 before madi_init). */
+int madi_device_cu_count(void);
+
+/* ---- Q8 layout (load time) ------------------------------------------------ */
+/* Natural -> panel layout, host memory to host memory.  Replaces nothing in
+ * the reference directly: it runs where the loader has just produced or read
+ * the Q8 rows (transcribe.zig:235-263 upVecQ8, :309-341 quantInto/readQ8,
+ * :377-410 upMatQ8/upQKVQ8enc, :434-465 upQKVQ8).  Needs no GPU. */
+int madi_q8_repack_host(void *dst_qs, void *dst_scales, const void *qs,
+                        const void *scales, uint32_t n, uint32_t k);
+/* Panel -> natural layout, host to host (inverse of madi_q8_repack_host). */
+int madi_q8_unpack_host(void *dst_qs, void *dst_scales, const void *tiled_qs,
+                        const void *tiled_scales, uint32_t n, uint32_t k);
+/* Natural -> panel layout, device to device (src and dst must not overlap). */
+int madi_q8_repack(void *dst_qs, void *dst_scales, const void *qs, const void *scales,
+                   uint32_t n, uint32_t k);
+
+/* ---- ops (device pointers, panel-layout weights) ---------------------------- */
+/* Q8 -> F16 [K][N] transposed dequant, bit-exact fp16_rne(q * s).  Replaces
+ * kDeq (engine/metal/encoder.zig:154-159) and deqW16 (transcribe.zig:4387-4393),
+ * kernel dequant_q8_f16 (engine/metal/kernels/q8_gemm.metal:12-27). */
+int madi_q8_dequant_f16(void *wdq, const void *qs, const void *scales, uint32_t n,
+                        uint32_t k);
+
+/* Fused Q8 GEMM: C[M][N] (f16) = epi(A[M][K] (f16) . deq(W)^T), fp32 accumulate.
+ * Argument order of m4_gemm_q8_bias_gelu (engine/metal/kernels/m4_gemm.metal:131-141);
+ * replaces the encoder's kDeq + kM4 / kM4Bias pairs (encoder.zig:125-136,
+ * 262-301) and mul_mm_q8 (q8_gemm.metal:29-102).  epilogue: NONE, BIAS or
+ * BIAS_GELU (bias may be NULL for NONE).  Requires N % 32 == 0, K % 64 == 0,
+ * 16-byte aligned A and C. */
+int madi_q8_gemm(const void *a, const void *qs, const void *scales, void *c,
+                 const float *bias, uint32_t m, uint32_t n, uint32_t k, int epilogue);
+
+/* Decoder GEMVs, x f32 [K] -> out f32 [N] (M = 1).  Argument order of the Zig
+ * wrappers (engine/metal/decoder.zig:155-181) with the Q8w struct spelled out as
+ * (qs, scales):
+ *   madi_q8_gemv            kGemvQ8          -> gemv_q8            graph_helpers.metal:390-419
+ *   madi_q8_gemv_bias       kGemvQ8Bias      -> gemv_q8_bias       graph_helpers.metal:424-451
+ *   madi_q8_gemv_bias_gelu  kGemvQ8BiasEpi   -> gemv_q8_bias_gelu  graph_helpers.metal:475-496
+ *   madi_q8_gemv_bias_res   kGemvQ8BiasEpi   -> gemv_q8_bias_res   graph_helpers.metal:498-519
+ * x must be 16-byte aligned; out may not alias x. */
+int madi_q8_gemv(float *out, const float *x, const void *qs, const void *scales,
+                 uint32_t n, uint32_t k);
+int madi_q8_gemv_bias(float *out, const float *x, const void *qs, const void *scales,
+                      const float *bias, uint32_t n, uint32_t k);
+int madi_q8_gemv_bias_gelu(float *out, const float *x, const void *qs, const void *scales,
+                           const float *bias, uint32_t n, uint32_t k);
+int madi_q8_gemv_bias_res(float *out, const float *x, const void *qs, const void *scales,
+                          const float *bias, uint32_t n, uint32_t k);
+/* Fused self-attention QKV: stacked [3D][D] weight, q_out = acc + qb, k -> kc[pos],
+ * v + vb -> vc[pos] with pos read on the device from *pos.  Replaces kQkv
+ * (decoder.zig:169-174) -> gemv_q8_qkv (graph_helpers.metal:527-558). */
+int madi_q8_gemv_qkv(float *q_out, const float *x, const void *qs, const void *scales,
+                     const float *qb, const float *vb, float *kc, float *vc,
+                     const uint32_t *pos, uint32_t d);
+/* Vocab logits over the tied Q8 embedding.  Replaces kLogitGemv
+ * (transcribe.zig:4369-4374) -> logit_gemv_q8 (graph_helpers.metal:320-351). */
+int madi_q8_logit_gemv(float *logits, const void *qs, const void *scales, const float *x,
+                       uint32_t vocab, uint32_t dim);
+/* GEMV with fp16 activations x [K] (the measured configuration: fp16 A,
+ * fp32 out).  epilogue: NONE, BIAS, BIAS_GELU or BIAS_RES.  No reference
+ * counterpart with this dtype; same arithmetic as madi_q8_gemv. */
+int madi_q8_gemv_f16x(float *out, const void *x_f16, const void *qs, const void *scales,
+                      const float *bias, uint32_t n, uint32_t k, int epilogue);
+
+/* Q8 embedding rows from the panel layout (the tied tok_emb the logit GEMV
+ * reads): out[d] = f32(q) * f32(s) for row *tok_ptr (gpu_emb_lookup_q8,
+ * graph_helpers.metal:370-383) or row tokens[*pos_ptr]
+ * (emb_lookup_indirect_q8, graph_helpers.metal:354-367).  The panel layout
+ * needs the table's row count (`vocab`) to place its last, partial panel; a
+ * token >= vocab writes nothing. */
+int madi_q8_emb_lookup(float *out, const void *qs, const void *scales,
+                       const uint32_t *tok_ptr, uint32_t vocab, uint32_t dim);
+int madi_q8_emb_lookup_indirect(float *out, const void *qs, const void *scales,
+                                const uint32_t *tokens, const uint32_t *pos_ptr,
+                                uint32_t vocab, uint32_t dim);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MADI_Q8_H */

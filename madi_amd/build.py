@@ -1,0 +1,64 @@
+"""Build recipe for the gfx950 Q8 matmul library (libmadi_q8.so).
+
+Compiles every HIP source under madi_amd/csrc with hipcc for gfx950 only and
+links them into one shared library next to this file, so the built library
+travels with the source tree.  Run as `python -m madi_amd.build`.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+CSRC = os.path.join(HERE, "csrc")
+OBJ_DIR = os.path.join(HERE, "_build")
+LIB = os.path.join(HERE, "libmadi_q8.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# Packed-fp32 VALU forms are kept out of every kernel: the library does its
+# fp32 work in scalar or vector-of-scalar code and lets no v_pk_*_f32 appear.
+HIP_FLAGS = [
+    "--offload-arch=gfx950",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I", os.path.join(ROOT, "include"),
+    "-I", CSRC,
+]
+
+
+def sources():
+    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def _run(cmd):
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
+    if r.returncode != 0:
+        sys.stderr.write(err + "\n")
+        raise RuntimeError(f"command failed ({r.returncode}): {' '.join(cmd)}")
+    return err
+
+
+def build(verbose: bool = False) -> str:
+    """Compile all sources and link libmadi_q8.so; returns the library path."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    objs = []
+    for src in sources():
+        obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + ".o")
+        msg = _run([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+        if verbose and msg.strip():
+            print(msg)
+        objs.append(obj)
+    tmp = LIB + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

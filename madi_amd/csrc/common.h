@@ -1,0 +1,93 @@
+// common.h -- shared host and device helpers of the gfx950 Q8 matmul library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "madi_q8.h"
+
+namespace madi {
+
+// ---------------------------------------------------------------- host side
+// Records a message for madi_last_error() and returns `code`.
+int fail(int code, const char *fmt, ...);
+int check_launch(const char *what);
+bool initialized();
+hipStream_t stream();
+
+inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// ---------------------------------------------------------------- device side
+typedef _Float16 f16;
+typedef f16 f16x2 __attribute__((ext_vector_type(2)));
+typedef f16 f16x4 __attribute__((ext_vector_type(4)));
+typedef f16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Panel layout geometry (see madi_q8.h).
+constexpr uint32_t kPanelRows = 32;
+constexpr uint32_t kChunkK = 64;
+
+__host__ __device__ inline uint32_t panel_rows(uint32_t n, uint32_t p) {
+  uint32_t left = n - p * kPanelRows;
+  return left < kPanelRows ? left : kPanelRows;
+}
+// byte offset of chunk c of panel p in the panel-layout qs buffer
+__host__ __device__ inline size_t panel_chunk_qs(uint32_t k, uint32_t p, uint32_t rows,
+                                                 uint32_t c) {
+  return (size_t)p * kPanelRows * k + (size_t)c * rows * kChunkK;
+}
+// element offset of chunk c of panel p in the panel-layout scales buffer
+__host__ __device__ inline size_t panel_chunk_sc(uint32_t k, uint32_t p, uint32_t rows,
+                                                 uint32_t c) {
+  return (size_t)p * kPanelRows * (k / 32) + (size_t)c * 2 * rows;
+}
+
+// Two biased bytes (q + 128) of `w`, selected by `sel`, to the exact fp16 pair
+// (q0, q1) times the fp16 scale pair `s2`.  The perm builds the fp16 bit
+// patterns 0x64uu = 1024 + u for each byte u, so x - 1152 = q exactly; one IEEE
+// fp16 multiply of the exact operands then gives fp16_rne(q * s), the
+// reference's half(float(q) * float(s)) (q8_gemm.metal:26) bit for bit.
+__device__ inline f16x2 dequant_pair(uint32_t w, uint32_t sel, f16x2 s2) {
+  uint32_t p = __builtin_amdgcn_perm(0x64646464u, w, sel);
+  f16x2 x = __builtin_bit_cast(f16x2, p);
+  const f16x2 bias = {(f16)-1152.0f, (f16)-1152.0f};
+  return (x + bias) * s2;
+}
+// byte selectors for v_perm_b32(0x64646464, w, sel): (b0,b1) and (b2,b3)
+constexpr uint32_t kSelLo = 0x04010400u;
+constexpr uint32_t kSelHi = 0x04030402u;
+
+// 16 biased bytes -> 16 dequantised fp16 (two MFMA k-steps of 8)
+__device__ inline void dequant16(const u32x4 &w, f16 s, f16x8 &lo, f16x8 &hi) {
+  const f16x2 s2 = {s, s};
+  f16x2 a0 = dequant_pair(w.x, kSelLo, s2), a1 = dequant_pair(w.x, kSelHi, s2);
+  f16x2 a2 = dequant_pair(w.y, kSelLo, s2), a3 = dequant_pair(w.y, kSelHi, s2);
+  f16x2 b0 = dequant_pair(w.z, kSelLo, s2), b1 = dequant_pair(w.z, kSelHi, s2);
+  f16x2 b2 = dequant_pair(w.w, kSelLo, s2), b3 = dequant_pair(w.w, kSelHi, s2);
+  lo = (f16x8){a0.x, a0.y, a1.x, a1.y, a2.x, a2.y, a3.x, a3.y};
+  hi = (f16x8){b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
+}
+
+// erf-form GELU, Abramowitz & Stegun 7.1.26, the formula of
+// engine/metal/kernels/graph_helpers.metal:460-473 and m4_gemm.metal:43-56.
+__device__ inline float gelu_erf(float xv) {
+  float z = xv * 0.7071067811865476f;
+  float az = __builtin_fabsf(z);
+  float sign = (z < 0.0f) ? -1.0f : 1.0f;
+  float t = 1.0f / __builtin_fmaf(az, 0.3275911f, 1.0f);
+  float poly = __builtin_fmaf(1.061405429f, t, -1.453152027f);
+  poly = __builtin_fmaf(poly, t, 1.421413741f);
+  poly = __builtin_fmaf(poly, t, -0.284496736f);
+  poly = __builtin_fmaf(poly, t, 0.254829592f);
+  poly = poly * t;
+  float ex = exp2f(__builtin_fmaxf(-az * az * 1.4426950408889634f, -80.0f));
+  float erf = sign * (1.0f - poly * ex);
+  return 0.5f * xv * (1.0f + erf);
+}
+
+}  // namespace madi

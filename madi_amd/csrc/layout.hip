@@ -1,0 +1,236 @@
+// layout.hip -- load-time repack into the CDNA4 panel layout, the transposed
+// F16 dequant, and Q8 embedding-row gathers, all on the panel layout.
+#include <string.h>
+
+#include "common.h"
+
+using namespace madi;
+
+namespace {
+
+int check_q8_shape(const char *what, uint32_t n, uint32_t k) {
+  if (n == 0 || k == 0) return fail(MADI_ERR_SHAPE, "%s: empty weight (n=%u k=%u)", what, n, k);
+  if (k % kChunkK != 0)
+    return fail(MADI_ERR_SHAPE, "%s: k=%u is not a multiple of %u (panel layout)", what, k, kChunkK);
+  return MADI_OK;
+}
+
+// natural index of the byte stored at panel-layout unit (p, c, j, h, r), byte i
+inline size_t natural_qs_index(uint32_t k, uint32_t p, uint32_t c, uint32_t j, uint32_t h,
+                               uint32_t r, uint32_t i) {
+  return (size_t)(p * kPanelRows + r) * k + c * kChunkK + h * 32 + j * 16 + i;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------------ host repack
+extern "C" int madi_q8_repack_host(void *dst_qs, void *dst_scales, const void *qs,
+                                   const void *scales, uint32_t n, uint32_t k) {
+  if (!dst_qs || !dst_scales || !qs || !scales) return fail(MADI_ERR_NULL, "madi_q8_repack_host: null pointer");
+  if (int rc = check_q8_shape("madi_q8_repack_host", n, k)) return rc;
+  const int8_t *src = static_cast<const int8_t *>(qs);
+  const uint16_t *ssrc = static_cast<const uint16_t *>(scales);
+  uint8_t *dst = static_cast<uint8_t *>(dst_qs);
+  uint16_t *sdst = static_cast<uint16_t *>(dst_scales);
+  const uint32_t np = (n + kPanelRows - 1) / kPanelRows, nc = k / kChunkK, nb = k / 32;
+  for (uint32_t p = 0; p < np; ++p) {
+    const uint32_t R = panel_rows(n, p);
+    for (uint32_t c = 0; c < nc; ++c) {
+      uint8_t *blk = dst + panel_chunk_qs(k, p, R, c);
+      uint16_t *sblk = sdst + panel_chunk_sc(k, p, R, c);
+      for (uint32_t j = 0; j < 2; ++j)
+        for (uint32_t h = 0; h < 2; ++h)
+          for (uint32_t r = 0; r < R; ++r) {
+            uint8_t *u = blk + ((2 * j + h) * R + r) * 16;
+            for (uint32_t i = 0; i < 16; ++i)
+              u[i] = (uint8_t)(src[natural_qs_index(k, p, c, j, h, r, i)] + 128);
+          }
+      for (uint32_t h = 0; h < 2; ++h)
+        for (uint32_t r = 0; r < R; ++r)
+          sblk[h * R + r] = ssrc[(size_t)(p * kPanelRows + r) * nb + 2 * c + h];
+    }
+  }
+  return MADI_OK;
+}
+
+extern "C" int madi_q8_unpack_host(void *dst_qs, void *dst_scales, const void *tiled_qs,
+                                   const void *tiled_scales, uint32_t n, uint32_t k) {
+  if (!dst_qs || !dst_scales || !tiled_qs || !tiled_scales)
+    return fail(MADI_ERR_NULL, "madi_q8_unpack_host: null pointer");
+  if (int rc = check_q8_shape("madi_q8_unpack_host", n, k)) return rc;
+  const uint8_t *src = static_cast<const uint8_t *>(tiled_qs);
+  const uint16_t *ssrc = static_cast<const uint16_t *>(tiled_scales);
+  int8_t *dst = static_cast<int8_t *>(dst_qs);
+  uint16_t *sdst = static_cast<uint16_t *>(dst_scales);
+  const uint32_t np = (n + kPanelRows - 1) / kPanelRows, nc = k / kChunkK, nb = k / 32;
+  for (uint32_t p = 0; p < np; ++p) {
+    const uint32_t R = panel_rows(n, p);
+    for (uint32_t c = 0; c < nc; ++c) {
+      const uint8_t *blk = src + panel_chunk_qs(k, p, R, c);
+      const uint16_t *sblk = ssrc + panel_chunk_sc(k, p, R, c);
+      for (uint32_t j = 0; j < 2; ++j)
+        for (uint32_t h = 0; h < 2; ++h)
+          for (uint32_t r = 0; r < R; ++r) {
+            const uint8_t *u = blk + ((2 * j + h) * R + r) * 16;
+            for (uint32_t i = 0; i < 16; ++i)
+              dst[natural_qs_index(k, p, c, j, h, r, i)] = (int8_t)(u[i] - 128);
+          }
+      for (uint32_t h = 0; h < 2; ++h)
+        for (uint32_t r = 0; r < R; ++r)
+          sdst[(size_t)(p * kPanelRows + r) * nb + 2 * c + h] = sblk[h * R + r];
+    }
+  }
+  return MADI_OK;
+}
+
+// ------------------------------------------------------------------ device repack
+// One thread per natural 16-byte unit (reads coalesced along the row).
+__global__ __launch_bounds__(256) void q8_repack_qs_kernel(uint8_t *__restrict__ dst,
+                                                           const int8_t *__restrict__ src,
+                                                           uint32_t n, uint32_t k,
+                                                           size_t units) {
+  size_t u = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= units) return;
+  const uint32_t upr = k / 16;
+  const uint32_t row = (uint32_t)(u / upr), kk = (uint32_t)(u % upr) * 16;
+  const uint32_t p = row / kPanelRows, r = row % kPanelRows, R = panel_rows(n, p);
+  const uint32_t c = kk / kChunkK, h = (kk % kChunkK) / 32, j = (kk % 32) / 16;
+  u32x4 w = *reinterpret_cast<const u32x4 *>(src + (size_t)row * k + kk);
+  w ^= (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};  // q + 128 per byte
+  *reinterpret_cast<u32x4 *>(dst + panel_chunk_qs(k, p, R, c) + ((2 * j + h) * R + r) * 16) = w;
+}
+
+__global__ __launch_bounds__(256) void q8_repack_sc_kernel(uint16_t *__restrict__ dst,
+                                                           const uint16_t *__restrict__ src,
+                                                           uint32_t n, uint32_t k,
+                                                           size_t count) {
+  size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (e >= count) return;
+  const uint32_t nb = k / 32;
+  const uint32_t row = (uint32_t)(e / nb), b = (uint32_t)(e % nb);
+  const uint32_t p = row / kPanelRows, r = row % kPanelRows, R = panel_rows(n, p);
+  const uint32_t c = b / 2, h = b % 2;
+  dst[panel_chunk_sc(k, p, R, c) + h * R + r] = src[e];
+}
+
+static bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
+  uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + nb && y < x + na;
+}
+
+extern "C" int madi_q8_repack(void *dst_qs, void *dst_scales, const void *qs, const void *scales,
+                              uint32_t n, uint32_t k) {
+  if (!dst_qs || !dst_scales || !qs || !scales) return fail(MADI_ERR_NULL, "madi_q8_repack: null pointer");
+  if (int rc = check_q8_shape("madi_q8_repack", n, k)) return rc;
+  if (!aligned(dst_qs, 16) || !aligned(qs, 16) || !aligned(dst_scales, 2) || !aligned(scales, 2))
+    return fail(MADI_ERR_ALIGN, "madi_q8_repack: qs buffers need 16-byte alignment");
+  const size_t nq = (size_t)n * k, ns = (size_t)n * (k / 32);
+  if (overlaps(dst_qs, nq, qs, nq) || overlaps(dst_scales, ns * 2, scales, ns * 2))
+    return fail(MADI_ERR_ARG, "madi_q8_repack: source and destination overlap");
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_repack: madi_init has not succeeded");
+  const size_t units = nq / 16;
+  hipLaunchKernelGGL(q8_repack_qs_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0,
+                     stream(), static_cast<uint8_t *>(dst_qs), static_cast<const int8_t *>(qs), n,
+                     k, units);
+  if (int rc = check_launch("madi_q8_repack(qs)")) return rc;
+  hipLaunchKernelGGL(q8_repack_sc_kernel, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0,
+                     stream(), static_cast<uint16_t *>(dst_scales),
+                     static_cast<const uint16_t *>(scales), n, k, ns);
+  return check_launch("madi_q8_repack(scales)");
+}
+
+// ------------------------------------------------------------------ dequant -> F16 [K][N]
+// grid (ceil(R*K/16 / 256), panels): one thread per panel-layout 16-byte unit.
+// Consecutive lanes hold consecutive rows r, so each of the 16 stores writes
+// 32 consecutive n of one output row k (coalesced 64-byte runs).
+__global__ __launch_bounds__(256) void q8_dequant_f16_kernel(f16 *__restrict__ out,
+                                                             const uint8_t *__restrict__ qs,
+                                                             const f16 *__restrict__ sc,
+                                                             uint32_t n, uint32_t k) {
+  const uint32_t p = blockIdx.y, R = panel_rows(n, p);
+  const uint32_t u = blockIdx.x * 256 + threadIdx.x;
+  if (u >= R * (k / 16)) return;
+  const uint32_t per_chunk = 4 * R;  // units per chunk
+  const uint32_t c = u / per_chunk, rem = u % per_chunk;
+  const uint32_t jh = rem / R, r = rem % R, j = jh / 2, h = jh % 2;
+  const u32x4 w = *reinterpret_cast<const u32x4 *>(qs + panel_chunk_qs(k, p, R, c) + rem * 16);
+  const f16 s = sc[panel_chunk_sc(k, p, R, c) + h * R + r];
+  f16x8 lo, hi;
+  dequant16(w, s, lo, hi);
+  const uint32_t col = p * kPanelRows + r;
+  const uint32_t k0 = c * kChunkK + h * 32 + j * 16;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    out[(size_t)(k0 + i) * n + col] = lo[i];
+    out[(size_t)(k0 + 8 + i) * n + col] = hi[i];
+  }
+}
+
+extern "C" int madi_q8_dequant_f16(void *wdq, const void *qs, const void *scales, uint32_t n,
+                                   uint32_t k) {
+  if (!wdq || !qs || !scales) return fail(MADI_ERR_NULL, "madi_q8_dequant_f16: null pointer");
+  if (int rc = check_q8_shape("madi_q8_dequant_f16", n, k)) return rc;
+  if (!aligned(qs, 16) || !aligned(scales, 2) || !aligned(wdq, 2))
+    return fail(MADI_ERR_ALIGN, "madi_q8_dequant_f16: qs needs 16-byte alignment");
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_dequant_f16: madi_init has not succeeded");
+  const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
+  const uint32_t units = kPanelRows * (k / 16);
+  hipLaunchKernelGGL(q8_dequant_f16_kernel, dim3((units + 255) / 256, np), dim3(256), 0,
+                     stream(), static_cast<f16 *>(wdq), static_cast<const uint8_t *>(qs),
+                     static_cast<const f16 *>(scales), n, k);
+  return check_launch("madi_q8_dequant_f16");
+}
+
+// ------------------------------------------------------------------ embedding rows
+__device__ inline float panel_weight(const uint8_t *qs, const f16 *sc, uint32_t n, uint32_t k,
+                                     uint32_t row, uint32_t d) {
+  const uint32_t p = row / kPanelRows, r = row % kPanelRows, R = panel_rows(n, p);
+  const uint32_t c = d / kChunkK, kk = d % kChunkK, h = kk / 32, j = (kk % 32) / 16, i = kk % 16;
+  const int q = (int)qs[panel_chunk_qs(k, p, R, c) + ((2 * j + h) * R + r) * 16 + i] - 128;
+  const float s = (float)sc[panel_chunk_sc(k, p, R, c) + h * R + r];
+  return (float)q * s;
+}
+
+// gpu_emb_lookup_q8 / emb_lookup_indirect_q8 semantics (graph_helpers.metal:354-383).
+// `n_rows` bounds the token: an out-of-range token writes nothing (the
+// reference reads out of bounds there; this build refuses instead).
+__global__ __launch_bounds__(256) void q8_emb_row_kernel(float *__restrict__ out,
+                                                         const uint8_t *__restrict__ qs,
+                                                         const f16 *__restrict__ sc,
+                                                         const uint32_t *__restrict__ tok_ptr,
+                                                         const uint32_t *__restrict__ tokens,
+                                                         const uint32_t *__restrict__ pos_ptr,
+                                                         uint32_t n_rows, uint32_t dim) {
+  const uint32_t tok = tokens ? tokens[pos_ptr[0]] : tok_ptr[0];
+  if (tok >= n_rows) return;
+  for (uint32_t d = threadIdx.x; d < dim; d += 256) out[d] = panel_weight(qs, sc, n_rows, dim, tok, d);
+}
+
+static int emb_common(const char *what, float *out, const void *qs, const void *scales,
+                      const uint32_t *tok_ptr, const uint32_t *tokens, const uint32_t *pos_ptr,
+                      uint32_t n_rows, uint32_t dim) {
+  if (!out || !qs || !scales) return fail(MADI_ERR_NULL, "%s: null pointer", what);
+  if (dim == 0 || dim % kChunkK) return fail(MADI_ERR_SHAPE, "%s: dim=%u must be a positive multiple of 64", what, dim);
+  if (n_rows == 0) return fail(MADI_ERR_SHAPE, "%s: empty table", what);
+  if (!aligned(qs, 16) || !aligned(scales, 2) || !aligned(out, 4))
+    return fail(MADI_ERR_ALIGN, "%s: misaligned pointer", what);
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);
+  hipLaunchKernelGGL(q8_emb_row_kernel, dim3(1), dim3(256), 0, stream(), out,
+                     static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), tok_ptr,
+                     tokens, pos_ptr, n_rows, dim);
+  return check_launch(what);
+}
+
+extern "C" int madi_q8_emb_lookup(float *out, const void *qs, const void *scales,
+                                  const uint32_t *tok_ptr, uint32_t vocab, uint32_t dim) {
+  if (!tok_ptr) return fail(MADI_ERR_NULL, "madi_q8_emb_lookup: null tok_ptr");
+  return emb_common("madi_q8_emb_lookup", out, qs, scales, tok_ptr, nullptr, nullptr, vocab, dim);
+}
+
+extern "C" int madi_q8_emb_lookup_indirect(float *out, const void *qs, const void *scales,
+                                           const uint32_t *tokens, const uint32_t *pos_ptr,
+                                           uint32_t vocab, uint32_t dim) {
+  if (!tokens || !pos_ptr) return fail(MADI_ERR_NULL, "madi_q8_emb_lookup_indirect: null pointer");
+  return emb_common("madi_q8_emb_lookup_indirect", out, qs, scales, nullptr, tokens, pos_ptr,
+                    vocab, dim);
+}

@@ -1,0 +1,134 @@
+// runtime.hip -- device selection, memory, stream ordering and error reporting.
+//
+// Replaces the Metal bridge's runtime half (engine/metal/metal_backend.h:15-69,
+// metal_backend.m:336-368 mtl_alloc/mtl_free).  One global device and stream,
+// like the bridge's one device/queue; see madi_q8.h for the contract.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "common.h"
+
+namespace madi {
+
+namespace {
+thread_local char g_err[512] = "";
+bool g_init = false;
+int g_cu_count = 0;
+hipStream_t g_stream = nullptr;
+}  // namespace
+
+int fail(int code, const char *fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char *what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(MADI_ERR_DISPATCH, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return MADI_OK;
+}
+
+bool initialized() { return g_init; }
+hipStream_t stream() { return g_stream; }
+
+}  // namespace madi
+
+using namespace madi;
+
+extern "C" int madi_init(void) {
+  if (g_init) return MADI_OK;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count < 1)
+    return fail(MADI_ERR_INIT, "madi_init: no HIP device (%s)", hipGetErrorString(e));
+  e = hipSetDevice(0);
+  if (e != hipSuccess) return fail(MADI_ERR_INIT, "madi_init: hipSetDevice: %s", hipGetErrorString(e));
+  hipDeviceProp_t prop;
+  e = hipGetDeviceProperties(&prop, 0);
+  if (e != hipSuccess)
+    return fail(MADI_ERR_INIT, "madi_init: hipGetDeviceProperties: %s", hipGetErrorString(e));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(MADI_ERR_INIT, "madi_init: device is %s, this library is built for gfx950",
+                prop.gcnArchName);
+  g_cu_count = prop.multiProcessorCount;
+  g_init = true;
+  g_err[0] = 0;
+  return MADI_OK;
+}
+
+extern "C" void madi_cleanup(void) {
+  if (!g_init) return;
+  (void)hipStreamSynchronize(g_stream);
+  g_stream = nullptr;
+  g_init = false;
+}
+
+extern "C" void *madi_alloc(size_t size) {
+  if (!g_init) {
+    fail(MADI_ERR_NOT_INIT, "madi_alloc: madi_init has not succeeded");
+    return nullptr;
+  }
+  if (size == 0) size = 1;
+  void *p = nullptr;
+  hipError_t e = hipMalloc(&p, size);
+  if (e != hipSuccess) {
+    fail(MADI_ERR_ALLOC, "madi_alloc(%zu): %s", size, hipGetErrorString(e));
+    return nullptr;
+  }
+  return p;
+}
+
+extern "C" void madi_free(void *ptr) {
+  if (!ptr || !g_init) return;
+  (void)hipFree(ptr);
+}
+
+extern "C" int madi_upload(void *dst, const void *src, size_t size) {
+  if (!g_init) return fail(MADI_ERR_NOT_INIT, "madi_upload: madi_init has not succeeded");
+  if (size == 0) return MADI_OK;
+  if (!dst || !src) return fail(MADI_ERR_NULL, "madi_upload: null pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, size, hipMemcpyHostToDevice, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  if (e != hipSuccess) return fail(MADI_ERR_SYNC, "madi_upload: %s", hipGetErrorString(e));
+  return MADI_OK;
+}
+
+extern "C" int madi_download(void *dst, const void *src, size_t size) {
+  if (!g_init) return fail(MADI_ERR_NOT_INIT, "madi_download: madi_init has not succeeded");
+  if (size == 0) return MADI_OK;
+  if (!dst || !src) return fail(MADI_ERR_NULL, "madi_download: null pointer");
+  hipError_t e = hipMemcpyAsync(dst, src, size, hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  if (e != hipSuccess) return fail(MADI_ERR_SYNC, "madi_download: %s", hipGetErrorString(e));
+  return MADI_OK;
+}
+
+extern "C" int madi_begin_command_buffer(void) {
+  if (!g_init) return fail(MADI_ERR_NOT_INIT, "madi_begin_command_buffer: not initialised");
+  return MADI_OK;
+}
+
+extern "C" int madi_commit_command_buffer(void) {
+  if (!g_init) return fail(MADI_ERR_NOT_INIT, "madi_commit_command_buffer: not initialised");
+  return check_launch("madi_commit_command_buffer");
+}
+
+extern "C" int madi_sync(void) {
+  if (!g_init) return fail(MADI_ERR_NOT_INIT, "madi_sync: madi_init has not succeeded");
+  hipError_t e = hipStreamSynchronize(g_stream);
+  if (e != hipSuccess) return fail(MADI_ERR_SYNC, "madi_sync: %s", hipGetErrorString(e));
+  return MADI_OK;
+}
+
+extern "C" int madi_set_stream(void *s) {
+  g_stream = reinterpret_cast<hipStream_t>(s);
+  return MADI_OK;
+}
+
+extern "C" const char *madi_last_error(void) { return g_err; }
+
+extern "C" int madi_device_cu_count(void) { return g_init ? g_cu_count : 0; }

@@ -1,0 +1,183 @@
+"""Python mirror of the engine's Q8 matmul operator wrappers, over the C ABI.
+
+Names, argument order and meaning follow the Zig wrappers the engine calls
+(engine/metal/encoder.zig:125-159, engine/metal/decoder.zig:155-181,
+engine/metal/transcribe.zig:4369-4393); a failing call raises MadiError, the
+counterpart of the wrappers' error{DispatchFailed, ...} returns
+(engine/metal/metal_backend.zig:34-41).  Pointers may be torch tensors (their
+device address is passed) or plain integers.  torch supplies device memory and
+the stream; all arithmetic runs in libmadi_q8.so.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+
+from ._lib import EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RES, EPI_NONE, call, check, lib
+
+D = 1280          # encoder.zig:12, decoder.zig:12
+MLP = 5120        # encoder.zig:15
+VOCAB = 51866     # decoder.zig:19
+ENC_SEQ = 1500    # encoder.zig:16
+
+
+def ptr(t) -> int | None:
+    if t is None:
+        return None
+    if isinstance(t, int):
+        return t
+    return t.data_ptr()
+
+
+def init(stream=None) -> None:
+    """madi_init (mtl_init) and order launches on `stream` (a torch stream, a raw
+    hipStream_t int, or None for torch's current stream)."""
+    call("madi_init")
+    if stream is None:
+        import torch
+        stream = torch.cuda.current_stream().cuda_stream
+    elif not isinstance(stream, int):
+        stream = stream.cuda_stream
+    call("madi_set_stream", stream)
+
+
+def sync() -> None:
+    call("madi_sync")
+
+
+@dataclass
+class Q8:
+    """A panel-layout Q8 weight on the device: {qs, scales} as in
+    engine/metal/encoder.zig:21 (Q8) and decoder.zig:22 (Q8w)."""
+    qs: int
+    scales: int
+    _keep: tuple = ()
+
+    def rows(self, row0: int, k: int) -> "Q8":
+        """The weight starting at row `row0` (a multiple of 32), as the engine slices
+        stacked q|k|v weights (encoder.zig:263-267)."""
+        assert row0 % 32 == 0, "panel layout slices at multiples of 32 rows"
+        return Q8(self.qs + row0 * k, self.scales + row0 * (k // 32) * 2, self._keep)
+
+
+def repack_host(qs: np.ndarray, scales: np.ndarray):
+    """Natural Q8 (int8 [N][K], f16 [N][K/32]) -> panel layout, on the host."""
+    n, k = qs.shape
+    qs = np.ascontiguousarray(qs, dtype=np.int8)
+    scales = np.ascontiguousarray(scales, dtype=np.float16)
+    tq = np.empty(n * k, dtype=np.uint8)
+    ts = np.empty(n * (k // 32), dtype=np.float16)
+    check(lib().madi_q8_repack_host(tq.ctypes.data, ts.ctypes.data, qs.ctypes.data,
+                                    scales.ctypes.data, n, k), "madi_q8_repack_host")
+    return tq, ts
+
+
+def unpack_host(tq: np.ndarray, ts: np.ndarray, n: int, k: int):
+    qs = np.empty((n, k), dtype=np.int8)
+    sc = np.empty((n, k // 32), dtype=np.float16)
+    check(lib().madi_q8_unpack_host(qs.ctypes.data, sc.ctypes.data,
+                                    np.ascontiguousarray(tq).ctypes.data,
+                                    np.ascontiguousarray(ts).ctypes.data, n, k),
+          "madi_q8_unpack_host")
+    return qs, sc
+
+
+def upload_q8(qs: np.ndarray, scales: np.ndarray, device="cuda") -> Q8:
+    """Load-time path: repack on the host, then copy to HBM.  Keeps the torch
+    buffers alive inside the returned Q8."""
+    import torch
+    tq, ts = repack_host(qs, scales)
+    dq = torch.from_numpy(tq).to(device)
+    ds = torch.from_numpy(ts.view(np.int16)).to(device)
+    return Q8(dq.data_ptr(), ds.data_ptr(), (dq, ds))
+
+
+def upload_q8_device_repack(qs: np.ndarray, scales: np.ndarray, device="cuda") -> Q8:
+    """Load-time path: copy the natural rows to HBM, repack there (madi_q8_repack)."""
+    import torch
+    n, k = qs.shape
+    nq = torch.from_numpy(np.ascontiguousarray(qs).view(np.uint8)).to(device)
+    ns = torch.from_numpy(np.ascontiguousarray(scales).view(np.int16)).to(device)
+    dq = torch.empty_like(nq)
+    ds = torch.empty_like(ns)
+    call("madi_q8_repack", dq.data_ptr(), ds.data_ptr(), nq.data_ptr(), ns.data_ptr(), n, k)
+    return Q8(dq.data_ptr(), ds.data_ptr(), (dq, ds, nq, ns))
+
+
+# ---- encoder.zig -----------------------------------------------------------
+def kDeq(wdq, w: Q8, n: int, k: int) -> None:
+    """encoder.zig:154-159: Q8 [N][K] -> F16 [K][N] (dequant_q8_f16)."""
+    call("madi_q8_dequant_f16", ptr(wdq), w.qs, w.scales, n, k)
+
+
+def deqW16(wdq, w: Q8, n: int, k: int) -> None:
+    """transcribe.zig:4387-4393: same operator as kDeq."""
+    kDeq(wdq, w, n, k)
+
+
+def kGemmQ8(a, w: Q8, c, m: int, n: int, k: int) -> None:
+    """Fused kDeq + kM4 (encoder.zig:125-130, 154-159): C = A . deq(W)^T, f16."""
+    call("madi_q8_gemm", ptr(a), w.qs, w.scales, ptr(c), None, m, n, k, EPI_NONE)
+
+
+def kGemmQ8Bias(a, w: Q8, c, bias, m: int, n: int, k: int, gelu: bool = False) -> None:
+    """Fused kDeq + kM4Bias (encoder.zig:131-136) with the m4_gemm_bias or
+    m4_gemm_bias_gelu epilogue (m4_gemm.metal:60-115)."""
+    call("madi_q8_gemm", ptr(a), w.qs, w.scales, ptr(c), ptr(bias), m, n, k,
+         EPI_BIAS_GELU if gelu else EPI_BIAS)
+
+
+# ---- decoder.zig -----------------------------------------------------------
+def kGemvQ8(out, x, w: Q8, n: int, k: int) -> None:
+    """decoder.zig:155-160 (gemv_q8)."""
+    call("madi_q8_gemv", ptr(out), ptr(x), w.qs, w.scales, n, k)
+
+
+def kGemvQ8Bias(out, x, w: Q8, bias, n: int, k: int) -> None:
+    """decoder.zig:162-167 (gemv_q8_bias)."""
+    call("madi_q8_gemv_bias", ptr(out), ptr(x), w.qs, w.scales, ptr(bias), n, k)
+
+
+def kGemvQ8BiasEpi(f: str, out, x, w: Q8, bias, n: int, k: int) -> None:
+    """decoder.zig:176-181; f = "gemv_q8_bias_gelu" or "gemv_q8_bias_res"."""
+    name = {"gemv_q8_bias_gelu": "madi_q8_gemv_bias_gelu",
+            "gemv_q8_bias_res": "madi_q8_gemv_bias_res"}[f]
+    call(name, ptr(out), ptr(x), w.qs, w.scales, ptr(bias), n, k)
+
+
+def kQkv(q_out, x, w: Q8, qb, vb, kc, vc, pos, d: int = D) -> None:
+    """decoder.zig:169-174 (gemv_q8_qkv); pos is a device u32."""
+    call("madi_q8_gemv_qkv", ptr(q_out), ptr(x), w.qs, w.scales, ptr(qb), ptr(vb), ptr(kc),
+         ptr(vc), ptr(pos), d)
+
+
+# ---- transcribe.zig ----------------------------------------------------------
+def kLogitGemv(logits, qs: int, sc: int, x, vocab: int = VOCAB, dim: int = D) -> None:
+    """transcribe.zig:4369-4374 (logit_gemv_q8)."""
+    call("madi_q8_logit_gemv", ptr(logits), qs, sc, ptr(x), vocab, dim)
+
+
+def embLookup(out, qs: int, sc: int, tok, vocab: int = VOCAB, dim: int = D) -> None:
+    """transcribe.zig:4361-4366 (gpu_emb_lookup_q8), tok a device u32."""
+    call("madi_q8_emb_lookup", ptr(out), qs, sc, ptr(tok), vocab, dim)
+
+
+def embLookupIndirect(out, qs: int, sc: int, tokens, pos, vocab: int = VOCAB,
+                      dim: int = D) -> None:
+    """emb_lookup_indirect_q8 (graph_helpers.metal:354-367)."""
+    call("madi_q8_emb_lookup_indirect", ptr(out), qs, sc, ptr(tokens), ptr(pos), vocab, dim)
+
+
+def gemv_f16x(out, x16, w: Q8, n: int, k: int, bias=None, epilogue: int = EPI_NONE) -> None:
+    """Q8 GEMV with fp16 activations (the measured decoder-GEMV configuration)."""
+    call("madi_q8_gemv_f16x", ptr(out), ptr(x16), w.qs, w.scales, ptr(bias), n, k, epilogue)
+
+
+__all__ = [
+    "D", "MLP", "VOCAB", "ENC_SEQ", "Q8", "init", "sync", "repack_host", "unpack_host",
+    "upload_q8", "upload_q8_device_repack", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias",
+    "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "kQkv", "kLogitGemv", "embLookup",
+    "embLookupIndirect", "gemv_f16x", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU",
+    "EPI_BIAS_RES",
+]

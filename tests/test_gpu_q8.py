@@ -1,0 +1,266 @@
+"""GPU parity of the gfx950 Q8 matmul path against the CPU oracle.
+
+Every call goes through the C ABI (libmadi_q8.so via ctypes); torch only
+provides device buffers.  Bars: bit-exact for the dequantised weights and the
+layout work; normwise max|C - C_ref| / max|C_ref| <= 1e-3 (the north-star
+tolerance) for the GEMM/GEMV, where C_ref is the oracle's
+dequantise-then-fp32-accumulate result.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from madi_amd import synth
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def q():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import madi_amd.q8 as q8
+    q8.init()
+    return q8
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def dev_f16(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float16).view(np.int16)).cuda()
+
+
+def host_f16(t):
+    return t.cpu().numpy().view(np.float16)
+
+
+def normwise(c, ref):
+    c = c.astype(np.float64)
+    ref = ref.astype(np.float64)
+    return np.max(np.abs(c - ref)) / max(np.max(np.abs(ref)), 1e-30)
+
+
+# ------------------------------------------------------------------ layout
+@pytest.mark.parametrize("n,k", [(64, 128), (100, 256), (51866, 1280)])
+def test_device_repack_matches_host(q, n, k):
+    say(f"repack n={n} k={k}")
+    rng = np.random.default_rng(n)
+    qs, sc = synth.q8_weight(rng, n, k)
+    tq, ts = q.repack_host(qs, sc)
+    w = q.upload_q8_device_repack(qs, sc)
+    q.sync()
+    dq, ds = w._keep[0], w._keep[1]
+    assert np.array_equal(dq.cpu().numpy(), tq)
+    assert np.array_equal(ds.cpu().numpy().view(np.float16).view(np.uint16), ts.view(np.uint16))
+
+
+@pytest.mark.parametrize("n,k", [(96, 128), (100, 256), (5120, 1280), (1280, 5120)])
+def test_dequant_bit_exact(q, n, k):
+    say(f"dequant n={n} k={k}")
+    rng = np.random.default_rng(k + n)
+    qs, sc = synth.q8_weight(rng, n, k)
+    # subnormal and large scales too: bit-exactness must not depend on the range
+    sc.flat[:8] = np.array([2**-24, 3 * 2**-24, 2**-14, 1e-5, 0.5, 1.0, 7.5, 300.0], np.float16)
+    w = q.upload_q8(qs, sc)
+    out = torch.empty((k, n), dtype=torch.int16, device="cuda")
+    q.kDeq(out, w, n, k)
+    q.sync()
+    ref = O.dequant_q8_f16(qs, sc)
+    assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+def test_stacked_row_slices(q):
+    """qkv slicing by pointer arithmetic (encoder.zig:263-267) on the panel layout."""
+    d = 256
+    rng = np.random.default_rng(3)
+    qs, sc = synth.q8_weight(rng, 3 * d, d)
+    w = q.upload_q8(qs, sc)
+    for blk in range(3):
+        out = torch.empty((d, d), dtype=torch.int16, device="cuda")
+        q.kDeq(out, w.rows(blk * d, d), d, d)
+        q.sync()
+        ref = O.dequant_q8_f16(qs[blk * d:(blk + 1) * d], sc[blk * d:(blk + 1) * d])
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
+
+
+# ------------------------------------------------------------------ GEMM
+def _gemm(q, a, qs, sc, bias=None, gelu=False):
+    m, k = a.shape
+    n = qs.shape[0]
+    w = q.upload_q8(qs, sc)
+    da = dev_f16(a)
+    dc = torch.empty((m, n), dtype=torch.int16, device="cuda")
+    if bias is None:
+        q.kGemmQ8(da, w, dc, m, n, k)
+    else:
+        q.kGemmQ8Bias(da, w, dc, dev(bias), m, n, k, gelu=gelu)
+    q.sync()
+    return host_f16(dc)
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (50, 64, 128),      # the reference's correctness shape (K rounded up to the 64-wide chunk)
+    (1, 256, 64),
+    (33, 512, 1280),
+    (100, 320, 192),    # N not a multiple of the 256-wide tile
+    (257, 1280, 1280),  # out-proj / per-head q,k,v shape, M tail
+])
+def test_gemm_parity_small(q, m, n, k):
+    say(f"gemm m={m} n={n} k={k}")
+    a, qs, sc = synth.gemm_case(m * 7 + n, m, n, k)
+    c = _gemm(q, a, qs, sc)
+    ref = O.q8_gemm_rows(a, qs, sc, threads=8)
+    assert normwise(c, ref) <= TOL, normwise(c, ref)
+    # elementwise: within fp16 output rounding plus accumulation-order noise
+    assert np.all(np.abs(c.astype(np.float64) - ref) <= 2**-10 * np.abs(ref) + 1e-4 * np.max(np.abs(ref)))
+
+
+def test_gemm_one_hot_is_dequant(q):
+    """A = identity rows: each output row is one dequantised weight column,
+    bit-exact (one exact product, fp32 sum of zeros, exact f16 store)."""
+    n, k = 256, 128
+    rng = np.random.default_rng(5)
+    qs, sc = synth.q8_weight(rng, n, k)
+    a = np.eye(k, dtype=np.float16)
+    c = _gemm(q, a, qs, sc)
+    ref = O.dequant_q8_f16(qs, sc)  # [K][N]
+    assert np.array_equal(c.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("gelu", [False, True])
+def test_gemm_bias_epilogues(q, gelu):
+    say(f"gemm bias gelu={gelu}")
+    m, n, k = 200, 768, 640
+    a, qs, sc = synth.gemm_case(11, m, n, k)
+    bias = np.random.default_rng(12).standard_normal(n).astype(np.float32)
+    c = _gemm(q, a, qs, sc, bias=bias, gelu=gelu)
+    ref = O.q8_gemm_rows(a, qs, sc, bias=bias,
+                         epilogue=O.EPI_BIAS_GELU if gelu else O.EPI_BIAS, threads=8)
+    assert normwise(c, ref) <= TOL
+
+
+@pytest.mark.parametrize("name,n,k", [("fc1", 5120, 1280), ("fc2", 1280, 5120), ("qkv", 3840, 1280)])
+def test_gemm_encoder_shapes_full_m(q, name, n, k):
+    """M = 1500 (one 30 s window); the oracle checks a row sample that covers
+    every M-tile boundary and the tail."""
+    say(f"gemm encoder {name} m=1500 n={n} k={k}")
+    m = 1500
+    a, qs, sc = synth.gemm_case(0, m, n, k)
+    c = _gemm(q, a, qs, sc)
+    rows = np.unique(np.r_[0, 1, 31, 32, 127, 128, 129, 767, 768, 1407, 1408, 1471, 1472,
+                           1498, 1499, np.random.default_rng(1).integers(0, m, 16)])
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, threads=16)
+    assert normwise(c[rows], ref) <= TOL
+    assert np.all(np.isfinite(c))
+
+
+# ------------------------------------------------------------------ GEMV
+@pytest.mark.parametrize("n,k", [(51866, 1280), (3840, 1280), (1280, 5120), (5120, 1280), (40, 64)])
+def test_gemv_parity(q, n, k):
+    say(f"gemv n={n} k={k}")
+    x16, qs, sc = synth.gemv_case(n + k, n, k)
+    x = x16.astype(np.float32)
+    w = q.upload_q8(qs, sc)
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    q.kGemvQ8(out, dev(x), w, n, k)
+    q.sync()
+    ref = O.q8_gemv(x, qs, sc, threads=8)
+    got = out.cpu().numpy()
+    assert normwise(got, ref) <= TOL
+    # f32 accumulation both sides: far tighter than the gate in practice
+    assert normwise(got, ref) <= 1e-5
+    # the fp16-activation entry point computes the same sums
+    out2 = torch.empty(n, dtype=torch.float32, device="cuda")
+    q.gemv_f16x(out2, dev_f16(x16), w, n, k)
+    q.sync()
+    assert normwise(out2.cpu().numpy(), ref) <= 1e-5
+
+
+def test_logit_gemv_vocab(q):
+    n, k = 51866, 1280
+    x16, qs, sc = synth.gemv_case(0, n, k)
+    x = x16.astype(np.float32)
+    w = q.upload_q8(qs, sc)
+    logits = torch.empty(n, dtype=torch.float32, device="cuda")
+    q.kLogitGemv(logits, w.qs, w.scales, dev(x), n, k)
+    q.sync()
+    ref = O.q8_gemv(x, qs, sc, threads=8)
+    got = logits.cpu().numpy()
+    assert normwise(got, ref) <= 1e-5
+    assert int(np.argmax(got)) == int(np.argmax(ref))
+
+
+@pytest.mark.parametrize("epi", ["bias", "gemv_q8_bias_gelu", "gemv_q8_bias_res"])
+def test_gemv_epilogues(q, epi):
+    n, k = 5120, 1280
+    x16, qs, sc = synth.gemv_case(7, n, k)
+    x = x16.astype(np.float32)
+    rng = np.random.default_rng(8)
+    bias = rng.standard_normal(n).astype(np.float32)
+    res0 = rng.standard_normal(n).astype(np.float32)
+    w = q.upload_q8(qs, sc)
+    out = dev(res0.copy())
+    if epi == "bias":
+        q.kGemvQ8Bias(out, dev(x), w, dev(bias), n, k)
+        ref = O.q8_gemv(x, qs, sc, bias, O.EPI_BIAS)
+    elif epi == "gemv_q8_bias_gelu":
+        q.kGemvQ8BiasEpi(epi, out, dev(x), w, dev(bias), n, k)
+        ref = O.q8_gemv(x, qs, sc, bias, O.EPI_BIAS_GELU)
+    else:
+        q.kGemvQ8BiasEpi(epi, out, dev(x), w, dev(bias), n, k)
+        ref = O.q8_gemv(x, qs, sc, bias, O.EPI_BIAS_RES, out=res0)
+    q.sync()
+    assert normwise(out.cpu().numpy(), ref) <= 1e-5
+
+
+def test_gemv_qkv_kv_store(q):
+    d = 1280
+    x16, qs, sc = synth.gemv_case(9, 3 * d, d)
+    x = x16.astype(np.float32)
+    rng = np.random.default_rng(10)
+    qb = rng.standard_normal(d).astype(np.float32)
+    vb = rng.standard_normal(d).astype(np.float32)
+    kc0 = np.full((8, d), 5.0, np.float32)
+    vc0 = np.full((8, d), -5.0, np.float32)
+    w = q.upload_q8(qs, sc)
+    qo = torch.empty(d, dtype=torch.float32, device="cuda")
+    kc, vc = dev(kc0.copy()), dev(vc0.copy())
+    pos = torch.tensor([6], dtype=torch.int32, device="cuda")
+    q.kQkv(qo, dev(x), w, dev(qb), dev(vb), kc, vc, pos, d)
+    q.sync()
+    rq, rk, rv = O.q8_gemv_qkv(x, qs, sc, qb, vb, kc0, vc0, 6)
+    assert normwise(qo.cpu().numpy(), rq) <= 1e-5
+    gk, gv = kc.cpu().numpy(), vc.cpu().numpy()
+    assert normwise(gk[6], rk[6]) <= 1e-5 and normwise(gv[6], rv[6]) <= 1e-5
+    others = np.r_[0:6, 7]
+    assert np.all(gk[others] == 5.0) and np.all(gv[others] == -5.0)
+
+
+def test_emb_lookup_rows(q):
+    n, k = 51866, 1280
+    rng = np.random.default_rng(21)
+    qs, sc = synth.q8_weight(rng, n, k)
+    w = q.upload_q8(qs, sc)
+    out = torch.empty(k, dtype=torch.float32, device="cuda")
+    for tok in (0, 31, 32, 50257, 51865):
+        t = torch.tensor([tok], dtype=torch.int32, device="cuda")
+        q.embLookup(out, w.qs, w.scales, t, n, k)
+        q.sync()
+        assert np.array_equal(out.cpu().numpy(), O.emb_row_q8(qs, sc, tok)), tok
+    toks = torch.tensor([7, 51864, 3], dtype=torch.int32, device="cuda")
+    pos = torch.tensor([1], dtype=torch.int32, device="cuda")
+    q.embLookupIndirect(out, w.qs, w.scales, toks, pos, n, k)
+    q.sync()
+    assert np.array_equal(out.cpu().numpy(), O.emb_row_q8(qs, sc, 51864))
