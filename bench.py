@@ -6,13 +6,21 @@ A step is one pass of the hot path over one batch of synthetic input:
   2. the decoder vocab-logit Q8 GEMV, x f16 [1280] x W int8 [51866, 1280] ->
      f32 logits [51866], cold: the step cycles through 4 distinct weight copies
      (4 x 70.75 MB > the 256 MB Infinity Cache) so each launch streams HBM.
-Inputs are resident in HBM before the timed region.  Each kernel launch is
-bracketed by HIP events on the stream it runs on; the JSON line reports the
-GEMM as the headline value (TFLOP/s) and the GEMV beside it (GB/s), each with
-its roofline fraction, plus the restated reference CPU path timed on this
-host's cores (a reported baseline only).
+Inputs are resident in HBM before the timed region.  The timed region runs
+the K steps' GEMMs back to back and then their GEMVs, with HIP events on the
+kernels' stream at the start, between the two runs and at the end, so each
+kernel's average duration is (event span) / K -- the figure rocprofv3's
+kernel trace reports for the same launches (a per-launch event pair would add
+the dispatch gap).  The JSON line reports the GEMM as the headline value
+(TFLOP/s) and the GEMV beside it (GB/s), each with its roofline fraction and,
+when profiles/traffic_q8_fc1_gemm_vocab_gemv.md holds them, the measured HBM
+bytes per launch, plus the restated reference CPU path timed on this host's
+cores (a reported baseline only).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+       python bench.py --calibrate-copy   (a plain 256 MiB device copy, the
+                                           reference kernel for FETCH_SIZE /
+                                           WRITE_SIZE scaling)
 """
 from __future__ import annotations
 
@@ -33,6 +41,8 @@ PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 M, K, N = 1500, 1280, 5120          # encoder fc1 at one 30 s window
 VOCAB, DIM = 51866, 1280            # decoder vocab logits
 GEMV_COPIES = 4
+COPY_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_q8_fc1_gemm_vocab_gemv.md")
 
 
 def log(msg):
@@ -59,12 +69,12 @@ def cpu_baseline(threads: int):
     from madi_amd import synth
     a, qs, sc = synth.gemm_case(0, M, N, K)
     res = {}
-    rows1 = np.arange(0, M, M // 96, dtype=np.uint32)[:96]
+    rows1 = np.arange(0, M, 3, dtype=np.uint32)[:480]
     O.q8_gemm_rows(a, qs, sc, rows=rows1[:2], threads=1)  # warm-up
     t = time.perf_counter()
     O.q8_gemm_rows(a, qs, sc, rows=rows1, threads=1)
     dt1 = time.perf_counter() - t
-    rowsn = np.arange(0, M, 2, dtype=np.uint32)[:480]
+    rowsn = np.arange(0, M, dtype=np.uint32)
     t = time.perf_counter()
     O.q8_gemm_rows(a, qs, sc, rows=rowsn, threads=threads)
     dtn = time.perf_counter() - t
@@ -74,18 +84,43 @@ def cpu_baseline(threads: int):
     x, qv, sv = synth.gemv_case(0, VOCAB, DIM)
     xf = x.astype(np.float32)
     t = time.perf_counter()
-    O.q8_gemv(xf, qv, sv, threads=1)
-    dtv1 = time.perf_counter() - t
-    t = time.perf_counter()
     for _ in range(3):
+        O.q8_gemv(xf, qv, sv, threads=1)
+    dtv1 = (time.perf_counter() - t) / 3
+    t = time.perf_counter()
+    for _ in range(10):
         O.q8_gemv(xf, qv, sv, threads=threads)
-    dtvn = (time.perf_counter() - t) / 3
+    dtvn = (time.perf_counter() - t) / 10
     res["gemv_1t_gbs"] = gemv_bytes() / dtv1 / 1e9
     res["gemv_nt_gbs"] = gemv_bytes() / dtvn / 1e9
-    res["sample"] = (f"fc1 GEMM: {rows1.size} of {M} rows single-thread ({dt1:.1f} s) and "
-                     f"{rowsn.size} rows on {threads} threads ({dtn:.1f} s), extrapolated per row; "
-                     f"vocab GEMV: full 1x{DIM}x{VOCAB}")
+    res["sample"] = (f"fc1 GEMM: {rows1.size} of {M} rows single-thread ({dt1:.1f} s, rate per row) "
+                     f"and all {rowsn.size} rows on {threads} threads ({dtn:.1f} s); vocab GEMV: "
+                     f"full 1x{DIM}x{VOCAB}, 3 runs single-thread, 10 on {threads} threads")
     return res
+
+
+def measured_traffic():
+    """HBM bytes per launch {kernel: bytes} from the committed PMC summary, if any."""
+    out = {}
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch"):
+                for kv in line.split()[1:]:
+                    k, v = kv.split("=")
+                    out[k] = float(v)
+    except OSError:
+        pass
+    return out
+
+
+def calibrate_copy():
+    import torch
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": COPY_BYTES, "launches": 5}))
 
 
 def cpu_model():
@@ -104,7 +139,12 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy (PMC calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        calibrate_copy()
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): the Q8 matmul "
               "path runs on a single MI355X; see DESIGN.md for how it would shard.",
@@ -132,35 +172,37 @@ def main():
     dlog = torch.empty(VOCAB, dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
 
-    def step(i, ev=None):
-        if ev is not None:
-            ev[0].record(stream)
+    def gemm(i):
         q8.kGemmQ8(da, wg, dc, M, N, K)
-        if ev is not None:
-            ev[1].record(stream)
+
+    def gemv(i):
         q8.gemv_f16x(dlog, dx, wv[i % GEMV_COPIES], VOCAB, DIM)
-        if ev is not None:
-            ev[2].record(stream)
 
     log(f"warmup {args.warmup} steps")
     for i in range(args.warmup):
-        step(i)
+        gemm(i)
+        gemv(i)
     torch.cuda.synchronize()
 
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
     log(f"timing {args.steps} steps")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
+    ev[0].record(stream)
     for i in range(args.steps):
-        step(i, evs[i])
+        gemm(i)
+    ev[1].record(stream)
+    for i in range(args.steps):
+        gemv(i)
+    ev[2].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    t_gemm = np.array([e[0].elapsed_time(e[1]) for e in evs]) * 1e-3   # s
-    t_gemv = np.array([e[1].elapsed_time(e[2]) for e in evs]) * 1e-3
-    g_avg, v_avg = float(t_gemm.mean()), float(t_gemv.mean())
+    g_avg = ev[0].elapsed_time(ev[1]) * 1e-3 / args.steps   # s per GEMM launch
+    v_avg = ev[1].elapsed_time(ev[2]) * 1e-3 / args.steps   # s per GEMV launch
     gemm_tflops = gemm_flops() / g_avg / 1e12
     gemv_gbs = gemv_bytes() / v_avg / 1e9
     ms_per_step = wall / args.steps * 1e3
+    traffic = measured_traffic()
     log(f"gemm {g_avg*1e6:.2f} us ({gemm_tflops:.1f} TFLOP/s), gemv {v_avg*1e6:.2f} us "
         f"({gemv_gbs:.0f} GB/s), wall {ms_per_step:.3f} ms/step")
 
@@ -185,15 +227,17 @@ def main():
         "roofline": {
             "bound": "mfma", "achieved": round(gemm_tflops, 2), "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(gemm_tflops / PEAK_FP16_TFLOPS, 4),
-            "traffic": None, "kernel": "q8_gemm_kernel", "avg_us": round(g_avg * 1e6, 3),
+            "traffic": traffic.get("q8_gemm_kernel"), "kernel": "q8_gemm_kernel",
+            "avg_us": round(g_avg * 1e6, 3),
             "algorithmic_per_launch": gemm_flops(),
         },
         "gemv": {
             "value": round(gemv_gbs, 1), "unit": "GB/s",
             "roofline": {
                 "bound": "hbm", "achieved": round(gemv_gbs, 1), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(gemv_gbs / PEAK_HBM_GBS, 4), "traffic": None,
-                "kernel": "q8_gemv_kernel", "avg_us": round(v_avg * 1e6, 3),
+                "unit": "GB/s", "frac": round(gemv_gbs / PEAK_HBM_GBS, 4),
+                "traffic": traffic.get("q8_gemv_kernel"), "kernel": "q8_gemv_kernel",
+                "avg_us": round(v_avg * 1e6, 3),
                 "algorithmic_per_launch": gemv_bytes(),
             },
         },

@@ -9,7 +9,8 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libmadi_q8.so")
+# MADI_Q8_LIB may point at another build of the same library (e.g. a tuning variant)
+LIB_PATH = os.environ.get("MADI_Q8_LIB", os.path.join(HERE, "libmadi_q8.so"))
 
 MADI_OK = 0
 ERRORS = {

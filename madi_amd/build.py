@@ -44,20 +44,21 @@ def _run(cmd):
     return err
 
 
-def build(verbose: bool = False) -> str:
-    """Compile all sources and link libmadi_q8.so; returns the library path."""
-    os.makedirs(OBJ_DIR, exist_ok=True)
+def build(verbose: bool = False, extra_flags=(), out: str = LIB, obj_dir: str = OBJ_DIR) -> str:
+    """Compile all sources and link the library (default libmadi_q8.so next to
+    this file); `extra_flags` (e.g. -D tuning macros) go to every compile."""
+    os.makedirs(obj_dir, exist_ok=True)
     objs = []
     for src in sources():
-        obj = os.path.join(OBJ_DIR, os.path.basename(src)[:-4] + ".o")
-        msg = _run([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+        obj = os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o")
+        msg = _run([HIPCC, *HIP_FLAGS, *extra_flags, "-c", src, "-o", obj])
         if verbose and msg.strip():
             print(msg)
         objs.append(obj)
-    tmp = LIB + ".tmp"
+    tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, out)
+    return out
 
 
 if __name__ == "__main__":

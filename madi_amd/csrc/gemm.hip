@@ -15,8 +15,10 @@
 // (global_load_lds_dwordx4, no VGPR staging):
 //   W  8 panels x 2 KiB int8 (the panel layout's chunk blocks, copied verbatim)
 //   S  8 panels x 128 B fp16 scales
-//   A  MT m-tiles x 4 k-steps x 1 KiB, in MFMA B-operand order (lane l holds
-//      A[m0 + 32i + l%32][k0 + 32(l/32) + 8s .. +8])
+//   A  32*MT rows x 128 B (64 f16), row-major with the 16-byte chunks of row r
+//      XOR-swizzled by (r >> 1) & 7; each DMA instruction copies 8 whole rows
+//      (eight 128-byte lines, fully coalesced), and the MFMA fragment reads
+//      (16 consecutive rows, one chunk each) hit 16 distinct bank groups
 // NSTAGES stages form a ring so loads run NSTAGES-1 chunks ahead of the math.
 // Wave w owns panels 2w, 2w+1: it reads its 2 x 2 KiB of int8 and 2 x 128 B of
 // scales, dequantises them in registers (v_perm_b32 + packed fp16 add/mul,
@@ -33,14 +35,18 @@ using namespace madi;
 namespace {
 
 constexpr int kPanelsPerTile = 8;
+constexpr int kWaves = 8;  // two waves per SIMD
 constexpr int kWBytes = kPanelsPerTile * 2048;
 constexpr int kSBytes = kPanelsPerTile * 128;
+constexpr int NSTAGES = 4;
 
 template <int MT>
 struct Geometry {
   static constexpr int kABytes = MT * 4 * 1024;
   static constexpr int kStage = kWBytes + kSBytes + kABytes;
-  static constexpr int kLoadsPerStage = 4 + MT + 1;  // per wave: W, A, S instructions
+  // DMA instructions per wave per stage: two weight halves of its panel, its
+  // share of the A row groups, and scales (see issue_stage)
+  static constexpr int kLoadsPerStage = MT == 1 ? 3 : 2 + MT / 2 + 1;
 };
 
 template <int N>
@@ -53,45 +59,91 @@ __device__ inline void dma16(const void *src, void *lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
 }
 
+// XOR swizzle of the A tile's 16-byte chunks within row `row`
+__device__ inline uint32_t a_swz(uint32_t row) { return (row >> 1) & 7; }
+
+// DMA of one ring stage (chunk c), in four parts.  Wave v copies: part 0/1,
+// the two 1 KiB halves of panel v's chunk block; part 2, its A row groups
+// (8 rows x 128 B each, fully coalesced) g = v, v+8, ... < 4*MT; part 3 the
+// scales: its own panel's 128 B (MT >= 2), or, for MT == 1 where waves 4..7
+// have no row group, 256 B covering panels 2(v-4), 2(v-4)+1.  Every wave
+// issues Geometry<MT>::kLoadsPerStage instructions per stage.  The parts ride
+// between the MFMAs of the four k-steps, so the vector-memory pipe drains
+// while the matrix pipe is busy.
 template <int MT>
-__device__ inline void issue_stage(uint8_t *stage, const f16 *__restrict__ A,
-                                   const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
-                                   uint32_t M, uint32_t K, uint32_t m0, uint32_t p0,
-                                   uint32_t np, uint32_t c, uint32_t wave, uint32_t lane) {
+__device__ inline void issue_part(uint8_t *stage, int part, const f16 *__restrict__ A,
+                                  const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
+                                  uint32_t M, uint32_t K, uint32_t m0, uint32_t p0, uint32_t np,
+                                  uint32_t c, uint32_t wave, uint32_t lane) {
   uint8_t *Ws = stage;
   uint8_t *Ss = stage + kWBytes;
   uint8_t *As = stage + kWBytes + kSBytes;
-  // W: wave w copies chunk blocks b = 4w..4w+3 (panel b/2, half b%2)
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t b = wave * 4 + i, t = b >> 1, j = b & 1;
-    uint32_t p = p0 + t;
+  if (part < 2) {
+    uint32_t p = p0 + wave;
     p = p < np ? p : np - 1;  // panels past N: valid bytes, results never stored
-    const uint8_t *src = qs + panel_chunk_qs(K, p, kPanelRows, c) + j * 1024 + lane * 16;
-    dma16(src, Ws + t * 2048 + j * 1024);
-  }
-  // A: wave w copies blocks b = w*MT .. w*MT+MT-1, block b = (m-tile b/4, step b%4)
-  const uint32_t h = lane >> 5, r = lane & 31;
+    dma16(qs + panel_chunk_qs(K, p, kPanelRows, c) + part * 1024 + lane * 16,
+          Ws + wave * 2048 + part * 1024);
+  } else if (part == 2) {
+    // lane l fills physical chunk l%8 of row 8g + l/8 with the logical chunk
+    // that the swizzle stores there
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    const uint32_t b = wave * MT + i, mi = b >> 2, s = b & 3;
-    uint32_t m = m0 + mi * 32 + r;
-    m = m < M ? m : M - 1;  // rows past M: valid bytes, results never stored
-    const f16 *src = A + (size_t)m * K + c * kChunkK + h * 32 + s * 8;
-    dma16(src, As + b * 1024);
-  }
-  // S: wave w copies the 2 x 128 B scale blocks of panels 2w, 2w+1 (16 lanes)
-  if (lane < 16) {
-    const uint32_t t = wave * 2 + (lane >> 3), q = lane & 7;
-    uint32_t p = p0 + t;
-    p = p < np ? p : np - 1;
-    const f16 *src = sc + panel_chunk_sc(K, p, kPanelRows, c) + q * 8;
-    dma16(src, Ss + wave * 256);
+    for (int g = (int)wave; g < 4 * MT; g += kWaves) {
+      const uint32_t row = g * 8 + (lane >> 3);
+      const uint32_t q = (lane & 7) ^ a_swz(row);
+      uint32_t m = m0 + row;
+      m = m < M ? m : M - 1;  // rows past M: valid bytes, results never stored
+      dma16(A + (size_t)m * K + c * kChunkK + q * 8, As + g * 1024);
+    }
+  } else {
+    if constexpr (MT == 1) {
+      if (wave >= 4 && lane < 16) {
+        const uint32_t t = (wave - 4) * 2 + (lane >> 3), q = lane & 7;
+        uint32_t pp = p0 + t;
+        pp = pp < np ? pp : np - 1;
+        dma16(sc + panel_chunk_sc(K, pp, kPanelRows, c) + q * 8, Ss + (wave - 4) * 256);
+      }
+    } else {
+      uint32_t p = p0 + wave;
+      p = p < np ? p : np - 1;
+      if (lane < 8) dma16(sc + panel_chunk_sc(K, p, kPanelRows, c) + lane * 8, Ss + wave * 128);
+    }
   }
 }
 
-template <int MT, int EPI, int NSTAGES>
-__global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
+template <int MT>
+__device__ inline void issue_stage(uint8_t *stage, const f16 *__restrict__ A,
+                                   const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
+                                   uint32_t M, uint32_t K, uint32_t m0, uint32_t p0, uint32_t np,
+                                   uint32_t c, uint32_t wave, uint32_t lane) {
+#pragma unroll
+  for (int part = 0; part < 4; ++part)
+    issue_part<MT>(stage, part, A, qs, sc, M, K, m0, p0, np, c, wave, lane);
+}
+
+// The MT activation fragments of k-step s from an A tile (swizzled rows).
+template <int MT>
+__device__ inline void load_a_frags(const uint8_t *As, int s, uint32_t h, uint32_t r,
+                                    f16x8 (&bf)[MT]) {
+  const uint32_t phys = ((h * 4 + s) ^ a_swz(r)) * 16;  // rows i*32 + r share (r >> 1) & 7
+#pragma unroll
+  for (int i = 0; i < MT; ++i)
+    bf[i] = *reinterpret_cast<const f16x8 *>(As + (i * 32 + r) * 128 + phys);
+}
+
+// One 16-byte weight unit (half j of this wave's panel) of the chunk in
+// `stage`, dequantised into two k-steps.
+__device__ inline void dequant_unit(const uint8_t *stage, uint32_t wave, uint32_t lane, int j,
+                                    f16 s, f16x8 &lo, f16x8 &hi) {
+  const u32x4 u = *reinterpret_cast<const u32x4 *>(stage + wave * 2048 + j * 1024 + lane * 16);
+  dequant16(u, s, lo, hi);
+}
+
+__device__ inline f16 panel_scale(const uint8_t *stage, uint32_t wave, uint32_t lane) {
+  return reinterpret_cast<const f16 *>(stage + kWBytes)[wave * 64 + lane];
+}
+
+template <int MT, int EPI>
+__global__ __launch_bounds__(512) void q8_gemm_kernel(const f16 *__restrict__ A,
                                                       const uint8_t *__restrict__ qs,
                                                       const f16 *__restrict__ sc,
                                                       f16 *__restrict__ Cout,
@@ -115,93 +167,100 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   const uint32_t tn = (bid % per_group) / gm;
 
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t h = lane >> 5, r = lane & 31;
   const uint32_t m0 = tm * 32 * MT, p0 = tn * kPanelsPerTile;
   const uint32_t np = N / kPanelRows, nchunks = K / kChunkK;
 
-  f32x16 acc[2][MT];
+  f32x16 acc[MT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int i = 0; i < MT; ++i) acc[t][i] = (f32x16){};
+  for (int i = 0; i < MT; ++i) acc[i] = (f32x16){};
 
+  // ---- software pipeline over a four-slot ring.  At iteration c: chunk c's
+  // activation fragments feed this iteration's MFMAs (its weights were
+  // dequantised during iteration c-1), chunk c+1's weights are dequantised
+  // between the MFMAs, chunk c+2 is in flight and chunk c+3 is issued, a part
+  // per k-step, into the slot chunk c-1 left (free once every wave passed
+  // this iteration's barrier).
 #pragma unroll
   for (int st = 0; st < NSTAGES - 1; ++st)
     if (st < (int)nchunks)
       issue_stage<MT>(smem + st * G::kStage, A, qs, sc, M, K, m0, p0, np, st, wave, lane);
+  if (nchunks >= 3)
+    wait_vmcnt<2 * G::kLoadsPerStage>();
+  else
+    wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+
+  f16x8 wcur[4], wnext[4];
+  {
+    const f16 s0 = panel_scale(smem, wave, lane);
+    dequant_unit(smem, wave, lane, 0, s0, wcur[0], wcur[1]);
+    dequant_unit(smem, wave, lane, 1, s0, wcur[2], wcur[3]);
+  }
+  f16x8 bcur[MT], bnext[MT];
+  load_a_frags<MT>(smem + kWBytes + kSBytes, 0, h, r, bcur);
 
   for (uint32_t c = 0; c < nchunks; ++c) {
-    // chunk c's DMA (this wave's part) has landed once at most the later
-    // stages' loads are outstanding; the barrier makes every wave's part visible
-    // and frees the slot the next issue overwrites.
-    if (c + NSTAGES - 2 < nchunks)
-      wait_vmcnt<(NSTAGES - 2) * G::kLoadsPerStage>();
-    else
-      wait_vmcnt<0>();
-    __builtin_amdgcn_s_barrier();
-    {
-      const uint32_t cn = c + NSTAGES - 1;
-      if (cn < nchunks)
-        issue_stage<MT>(smem + (cn % NSTAGES) * G::kStage, A, qs, sc, M, K, m0, p0, np, cn,
-                        wave, lane);
+    if (c + 1 < nchunks) {
+      // chunk c+1 has landed once only chunk c+2's loads may be outstanding;
+      // the barrier publishes every wave's part and retires slot c-1
+      if (c + 2 < nchunks)
+        wait_vmcnt<G::kLoadsPerStage>();
+      else
+        wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
     }
-    const uint8_t *stage = smem + (c % NSTAGES) * G::kStage;
-    const uint8_t *Ws = stage;
-    const f16 *Ss = reinterpret_cast<const f16 *>(stage + kWBytes);
-    const uint8_t *As = stage + kWBytes + kSBytes;
-
-    f16x8 wf[2][4];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint32_t tp = wave * 2 + t;
-      const u32x4 u0 = *reinterpret_cast<const u32x4 *>(Ws + tp * 2048 + lane * 16);
-      const u32x4 u1 = *reinterpret_cast<const u32x4 *>(Ws + tp * 2048 + 1024 + lane * 16);
-      const f16 s = Ss[tp * 64 + lane];
-      dequant16(u0, s, wf[t][0], wf[t][1]);
-      dequant16(u1, s, wf[t][2], wf[t][3]);
-    }
+    const bool refill = c + 3 < nchunks;  // chunk c+3's DMA rides between the steps
+    uint8_t *Rs = smem + ((c + 3) % NSTAGES) * G::kStage;
+    // Branch-free compute region; on the last chunk the "next" slot holds
+    // stale, in-bounds bytes whose dequantised values are never used.
+    const uint8_t *As = smem + (c % NSTAGES) * G::kStage + kWBytes + kSBytes;
+    const uint8_t *Wn = smem + ((c + 1) % NSTAGES) * G::kStage;
+    const uint8_t *An = Wn + kWBytes + kSBytes;
+    const f16 snext = panel_scale(Wn, wave, lane);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      f16x8 bf[MT];
+      if (s < 3)
+        load_a_frags<MT>(As, s + 1, h, r, bnext);
+      else
+        load_a_frags<MT>(An, 0, h, r, bnext);
+      if (s == 1) dequant_unit(Wn, wave, lane, 0, snext, wnext[0], wnext[1]);
+      if (s == 3) dequant_unit(Wn, wave, lane, 1, snext, wnext[2], wnext[3]);
 #pragma unroll
       for (int i = 0; i < MT; ++i)
-        bf[i] = *reinterpret_cast<const f16x8 *>(As + (i * 4 + s) * 1024 + lane * 16);
+        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wcur[s], bcur[i], acc[i], 0, 0, 0);
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < MT; ++i)
-          acc[t][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf[t][s], bf[i], acc[t][i], 0, 0, 0);
+      for (int i = 0; i < MT; ++i) bcur[i] = bnext[i];
+      if (refill) issue_part<MT>(Rs, s, A, qs, sc, M, K, m0, p0, np, c + 3, wave, lane);
     }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) wcur[s] = wnext[s];
   }
 
   // ---- epilogue: lane holds D[n][m] for m = l%32, n = 8g + 4(l/32) + (0..3)
-  const uint32_t h = lane >> 5, col = lane & 31;
+  const uint32_t nb = (p0 + wave) * kPanelRows;
+  if (nb >= N) return;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const uint32_t nb = (p0 + wave * 2 + t) * kPanelRows;
-    if (nb >= N) continue;
+  for (int i = 0; i < MT; ++i) {
+    const uint32_t m = m0 + i * 32 + r;
+    if (m >= M) continue;
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
-      const uint32_t m = m0 + i * 32 + col;
-      if (m >= M) continue;
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t n = nb + g * 8 + h * 4;
+      float v[4] = {acc[i][g * 4 + 0], acc[i][g * 4 + 1], acc[i][g * 4 + 2], acc[i][g * 4 + 3]};
+      if constexpr (EPI != MADI_EPI_NONE) {
+        const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bias + n);
+        v[0] += b4.x;
+        v[1] += b4.y;
+        v[2] += b4.z;
+        v[3] += b4.w;
+        if constexpr (EPI == MADI_EPI_BIAS_GELU) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const uint32_t n = nb + g * 8 + h * 4;
-        float v[4] = {acc[t][i][g * 4 + 0], acc[t][i][g * 4 + 1], acc[t][i][g * 4 + 2],
-                      acc[t][i][g * 4 + 3]};
-        if constexpr (EPI != MADI_EPI_NONE) {
-          const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bias + n);
-          v[0] += b4.x;
-          v[1] += b4.y;
-          v[2] += b4.z;
-          v[3] += b4.w;
-          if constexpr (EPI == MADI_EPI_BIAS_GELU) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
-          }
+          for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
         }
-        const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-        *reinterpret_cast<f16x4 *>(Cout + (size_t)m * N + n) = o;
       }
+      const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+      *reinterpret_cast<f16x4 *>(Cout + (size_t)m * N + n) = o;
     }
   }
 }
@@ -209,11 +268,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
 template <int MT, int EPI>
 int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const float *bias,
                 uint32_t M, uint32_t N, uint32_t K) {
-  constexpr int NSTAGES = MT >= 4 ? 3 : 4;
   const uint32_t tiles_m = (M + 32 * MT - 1) / (32 * MT);
   const uint32_t tiles_n = (N + 255) / 256;
   const uint32_t group_m = tiles_m < 6 ? tiles_m : 6;
-  hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, NSTAGES>), dim3(tiles_m * tiles_n), dim3(256), 0,
+  hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI>), dim3(tiles_m * tiles_n), dim3(kWaves * 64), 0,
                      stream(), A, qs, sc, C, bias, M, N, K, tiles_m, tiles_n, group_m);
   return check_launch("madi_q8_gemm");
 }

@@ -20,8 +20,14 @@ using namespace madi;
 
 namespace {
 
-constexpr int kPanelsPerWG = 2;
-constexpr int kUnroll = 4;  // chunks whose loads are in flight together
+#ifndef MADI_GEMV_PPW
+#define MADI_GEMV_PPW 1
+#endif
+#ifndef MADI_GEMV_UNROLL
+#define MADI_GEMV_UNROLL 5
+#endif
+constexpr int kPanelsPerWG = MADI_GEMV_PPW;
+constexpr int kUnroll = MADI_GEMV_UNROLL;  // chunks whose loads are in flight together
 constexpr uint32_t kMaxK = 12288;
 
 enum GemvMode { kPlain = 0, kBias = 1, kBiasGelu = 2, kBiasRes = 3, kQkv = 4 };
@@ -41,6 +47,29 @@ struct GemvArgs {
 
 __device__ inline float byte_f(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
 
+struct Batch {
+  u32x4 w[kUnroll][kPanelsPerWG][2];
+  f16 s[kUnroll][kPanelsPerWG];
+};
+
+// Issue the loads of chunks [c, min(c + kUnroll, c1)) of the workgroup's panels.
+__device__ inline void load_batch(Batch &b, const GemvArgs &a, uint32_t K, uint32_t c,
+                                  uint32_t c1, uint32_t p0, const uint32_t *R, const bool *live,
+                                  uint32_t h, uint32_t r) {
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u)
+#pragma unroll
+    for (int t = 0; t < kPanelsPerWG; ++t) {
+      if (c + u < c1 && live[t]) {
+        const uint32_t p = p0 + t, Rt = R[t];
+        const uint8_t *blk = a.qs + panel_chunk_qs(K, p, Rt, c + u);
+        b.w[u][t][0] = *reinterpret_cast<const u32x4 *>(blk + (h * Rt + r) * 16);
+        b.w[u][t][1] = *reinterpret_cast<const u32x4 *>(blk + ((2 + h) * Rt + r) * 16);
+        b.s[u][t] = a.sc[panel_chunk_sc(K, p, Rt, c + u) + h * Rt + r];
+      }
+    }
+}
+
 template <typename XT, int MODE>
 __global__ __launch_bounds__(256) void q8_gemv_kernel(GemvArgs a) {
   extern __shared__ float smem[];
@@ -48,16 +77,6 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(GemvArgs a) {
   float *xs = smem;                 // [K]
   float *xsum = smem + K;           // [C][2]: sum of each 32-wide half-chunk
   float *red = xsum + 2 * C;        // [4 waves][kPanelsPerWG * 32]
-
-  const XT *x = static_cast<const XT *>(a.x);
-  for (uint32_t i = threadIdx.x; i < K; i += 256) xs[i] = (float)x[i];
-  __syncthreads();
-  for (uint32_t i = threadIdx.x; i < 2 * C; i += 256) {
-    float s = 0.0f;
-    for (int e = 0; e < 32; ++e) s += xs[i * 32 + e];
-    xsum[i] = s;
-  }
-  __syncthreads();
 
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t h = lane >> 5, r = lane & 31;
@@ -72,25 +91,28 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(GemvArgs a) {
     R[t] = p < np ? panel_rows(a.n, p) : 0;
     live[t] = r < R[t];
   }
-
   const uint32_t c0 = (wave * C) / 4, c1 = ((wave + 1) * C) / 4;
-  float acc[kPanelsPerWG] = {};
 
+  // The first weight batch does not depend on x: put it in flight before the
+  // x prologue so the activation staging hides under HBM latency.
+  Batch b;
+  load_batch(b, a, K, c0, c1, p0, R, live, h, r);
+
+  // Stage x as f32; each 32-lane group also reduces one 32-wide block sum.
+  const XT *x = static_cast<const XT *>(a.x);
+  for (uint32_t i = threadIdx.x; i < K; i += 256) {
+    const float v = (float)x[i];
+    xs[i] = v;
+    float sum = v;
+#pragma unroll
+    for (int off = 16; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 32);
+    if ((i & 31) == 0) xsum[i >> 5] = sum;
+  }
+  __syncthreads();
+
+  float acc[kPanelsPerWG] = {};
   for (uint32_t c = c0; c < c1; c += kUnroll) {
-    u32x4 w[kUnroll][kPanelsPerWG][2];
-    f16 s[kUnroll][kPanelsPerWG];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
-#pragma unroll
-      for (int t = 0; t < kPanelsPerWG; ++t) {
-        if (c + u < c1 && live[t]) {
-          const uint32_t p = p0 + t, Rt = R[t];
-          const uint8_t *blk = a.qs + panel_chunk_qs(K, p, Rt, c + u);
-          w[u][t][0] = *reinterpret_cast<const u32x4 *>(blk + (h * Rt + r) * 16);
-          w[u][t][1] = *reinterpret_cast<const u32x4 *>(blk + ((2 + h) * Rt + r) * 16);
-          s[u][t] = a.sc[panel_chunk_sc(K, p, Rt, c + u) + h * Rt + r];
-        }
-      }
+    if (c != c0) load_batch(b, a, K, c, c1, p0, R, live, h, r);
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (c + u >= c1) break;
@@ -105,7 +127,7 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(GemvArgs a) {
         float part = 0.0f;
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-          const u32x4 ww = w[u][t][j];
+          const u32x4 ww = b.w[u][t][j];
           const uint32_t wd[4] = {ww.x, ww.y, ww.z, ww.w};
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
@@ -117,7 +139,7 @@ __global__ __launch_bounds__(256) void q8_gemv_kernel(GemvArgs a) {
           }
         }
         part = __builtin_fmaf(-128.0f, xsm, part);
-        acc[t] = __builtin_fmaf(part, (float)s[u][t], acc[t]);
+        acc[t] = __builtin_fmaf(part, (float)b.s[u][t], acc[t]);
       }
     }
   }
