@@ -7,27 +7,50 @@
 // (kernels/m4_gemm.metal:131-189).
 //
 // Workgroup tile: 256 weight rows (8 panels) x 32*MT activation rows, four
-// waves.  The weight is the MFMA A operand (rows = n) and the activations the
-// B operand (columns = m), so each lane's 16 fp32 results cover four runs of
-// four consecutive n and are stored as 8-byte f16x4 writes.
+// waves, one per SIMD.  Wave w owns panels 2w, 2w+1 and all MT m-tiles, so per
+// 16-wide k-step it runs 2*MT independent 32x32x16 MFMAs on two dequantised
+// weight fragments and MT activation fragments.  The weight is the MFMA A
+// operand (rows = n) and the activations the B operand (columns = m).
 //
-// Per 64-wide K chunk a stage of LDS holds, all written by direct-to-LDS DMA
-// (global_load_lds_dwordx4, no VGPR staging):
-//   W  8 panels x 2 KiB int8 (the panel layout's chunk blocks, copied verbatim)
-//   S  8 panels x 128 B fp16 scales
-//   A  32*MT rows x 128 B (64 f16), row-major with the 16-byte chunks of row r
-//      XOR-swizzled by (r >> 1) & 7; each DMA instruction copies 8 whole rows
-//      (eight 128-byte lines, fully coalesced), and the MFMA fragment reads
-//      (16 consecutive rows, one chunk each) hit 16 distinct bank groups
-// NSTAGES stages form a ring so loads run NSTAGES-1 chunks ahead of the math.
-// Wave w owns panels 2w, 2w+1: it reads its 2 x 2 KiB of int8 and 2 x 128 B of
-// scales, dequantises them in registers (v_perm_b32 + packed fp16 add/mul,
-// bit-exact fp16_rne(q*s)) and runs 2 x MT x 4 MFMAs per chunk.
+// Data movement per 64-wide K chunk:
+//   weights  each wave streams its own two panels straight into VGPRs
+//            (buffer_load_dwordx4: one contiguous KiB per instruction; in the
+//            panel layout lane (h, r) receives row r's 32 weights of
+//            quantisation block h) plus one fp16 scale per lane per panel, WD
+//            chunks ahead of use, into WD rotating register sets;
+//   A        the 32*MT x 64 f16 activation tile is shared by the four waves
+//            through an NA-stage LDS ring, written by direct-to-LDS DMA
+//            (buffer_load_dwordx4 ... lds) NA-1 chunks ahead; the 16-byte
+//            chunks of row r are XOR-swizzled by (r >> 1) & 7 so each DMA
+//            instruction copies 8 whole 128-byte rows and the fragment reads
+//            (32 consecutive rows, one chunk each) spread over all banks.
+// One barrier per chunk (before its last k-step) publishes the next chunk's A
+// stage and retires the oldest one.
+//
+// Weight fragments: register w[t][s] holds panel t's k-step-s fragment.  It
+// is consumed by the MFMAs of step s and refilled in place with the next
+// chunk's fragment right after them (w[0][s] during step s, w[1][s] during
+// step s+1), half a 16-byte unit at a time: v_perm_b32 builds the fp16
+// values 1024 + (q + 128), a packed subtract makes them q exactly and a
+// packed multiply by the scale rounds once, so each weight is the reference's
+// half(float(q) * float(s)) (q8_gemm.metal:26) bit for bit.  Every k-step
+// issues its next-step LDS reads first and then alternates one MFMA with
+// three dequantisation VALU ops (fixed with sched_group_barrier), so the
+// matrix pipe is never left waiting on the vector ALU.
 //
 // K ordering: MFMA k-slot (lane half h, slot e) of step s holds k = 32h + 8s + e
 // for BOTH operands, so each lane's weight slice of a chunk lies in one
-// quantisation block (one scale per lane per chunk); any k permutation shared
-// by both operands leaves the product unchanged.
+// quantisation block (one scale per lane per panel per chunk); any k
+// permutation shared by both operands leaves the product unchanged.
+//
+// The chunk count is padded to a multiple of WD with empty chunks: their
+// loads use a zero-length buffer resource, which returns zeros without
+// touching memory, so they add exact zeros.  Loads are issued in the same
+// pattern every chunk, which keeps every vmcnt wait a constant.
+//
+// Epilogue: bias / GELU in fp32 registers, one rounding to f16, then the tile
+// is transposed through LDS so every global store writes whole 512-byte row
+// segments (16 bytes per lane).
 #include "common.h"
 
 using namespace madi;
@@ -35,92 +58,143 @@ using namespace madi;
 namespace {
 
 constexpr int kPanelsPerTile = 8;
-constexpr int kWaves = 8;  // two waves per SIMD
-constexpr int kWBytes = kPanelsPerTile * 2048;
-constexpr int kSBytes = kPanelsPerTile * 128;
-constexpr int NSTAGES = 4;
+constexpr int kWaves = 4;  // one wave per SIMD
+constexpr int NA = 4;      // activation ring stages
+constexpr int WD = 4;      // weight register sets (chunks of weight prefetch)
+constexpr int kCStride = kPanelsPerTile * kPanelRows * 2 + 16;  // epilogue tile row pitch
 
 template <int MT>
 struct Geometry {
-  static constexpr int kABytes = MT * 4 * 1024;
-  static constexpr int kStage = kWBytes + kSBytes + kABytes;
-  // DMA instructions per wave per stage: two weight halves of its panel, its
-  // share of the A row groups, and scales (see issue_stage)
-  static constexpr int kLoadsPerStage = MT == 1 ? 3 : 2 + MT / 2 + 1;
+  static constexpr int kStage = MT * 32 * 128;  // one A stage (32*MT rows x 64 f16)
+  static constexpr int kRing = NA * kStage;
+  static constexpr int kCTile = 32 * MT * kCStride;
+  static constexpr int kLds = kRing > kCTile ? kRing : kCTile;
+  // vector-memory instructions per wave per chunk, spread over the four
+  // k-steps so the texture pipe never sees a burst: step 0 the first half of
+  // the A DMA (MT row groups of 8 rows), step 1 its second half and weight unit
+  // (0,0), step 2 units (0,1) and (1,0), step 3 unit (1,1) and the two scales
+  static constexpr int LA = MT;
+  static constexpr int LW = 6;
+  static constexpr int kPerChunk = LA + LW;
+  static constexpr int kBeforeStep3 = LA + 3;  // issued in steps 0..2
+  // at the start of chunk c: the weights of chunk c+1 (the last loads of
+  // chunk c+1-WD) have landed once only the loads of the WD-2 chunks after
+  // them are outstanding
+  static constexpr int kVmRaw = (WD - 2) * kPerChunk;
+  // before step 3 of chunk c: chunk c+1's A stage (issued in steps 0-1 of
+  // chunk c+2-NA, followed by 6 weight loads) has landed
+  static constexpr int kVmA = LW + (NA - 3) * kPerChunk + kBeforeStep3;
+  // prologue: virtual chunks -WD..-1 issue the same pattern; chunk 0's A stage
+  // (virtual chunk 1-NA) and weights (virtual chunk -WD) have landed
+  static constexpr int kVmPrologue = LW + (NA - 2) * kPerChunk;
+  static_assert(kVmRaw < 64 && kVmA < 64, "vmcnt range");
 };
 
-template <int N>
-__device__ inline void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// Every vector-memory instruction of the kernel is issued from inline asm, so
+// the compiler inserts no vmcnt waits of its own (its conservative counts
+// stalled on loads issued chunks later); the kernel waits explicitly with the
+// exact counts of its fixed issue pattern.  M0 is written only here.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+
+// Raw (stride 0) buffer descriptor over [base, base + bytes): SGPR words.
+// bytes = 0 gives a descriptor whose every load returns zeros without
+// touching memory.  Range checks cover the per-lane offset only, so every
+// real load keeps its address in bounds by construction.
+typedef u32x4 desc_t;
+__device__ inline desc_t make_desc(const void *base, uint32_t bytes) {
+  const uint64_t b = reinterpret_cast<uint64_t>(base);
+  return (desc_t){(uint32_t)b, (uint32_t)(b >> 32) & 0xffffu, bytes, 0x00020000u};
 }
 
-__device__ inline void dma16(const void *src, void *lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_wave_base, 16, 0, 0);
+// 16 bytes per lane at soff + voff into VGPRs.
+__device__ inline void vload16(u32x4 &v, desc_t d, uint32_t voff, uint32_t soff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff));
+}
+// 2 bytes per lane (zero-extended) at soff + voff into a VGPR.
+__device__ inline void vload2(uint32_t &v, desc_t d, uint32_t voff, uint32_t soff) {
+  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff));
+}
+// One wave-wide DMA of 16 bytes per lane: buffer bytes [soff + voff, +16) ->
+// LDS lds + 16*lane.
+__device__ inline void dma16(desc_t d, uint32_t voff, uint32_t soff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               ::"s"(lds), "v"(voff), "s"(d), "s"(soff) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+__device__ inline uint32_t lds_addr(const uint8_t *p) {
+  return (uint32_t)(uintptr_t)(const lds_u8 *)p;
+}
+
+// Wait until at most N of this wave's vector-memory ops and none of its LDS
+// reads are outstanding, then meet the other waves.  One asm statement, so no
+// LDS access can be scheduled between the wait and the barrier.
+template <int N>
+__device__ inline void wait_then_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
 // XOR swizzle of the A tile's 16-byte chunks within row `row`
 __device__ inline uint32_t a_swz(uint32_t row) { return (row >> 1) & 7; }
 
-// DMA of one ring stage (chunk c), in four parts.  Wave v copies: part 0/1,
-// the two 1 KiB halves of panel v's chunk block; part 2, its A row groups
-// (8 rows x 128 B each, fully coalesced) g = v, v+8, ... < 4*MT; part 3 the
-// scales: its own panel's 128 B (MT >= 2), or, for MT == 1 where waves 4..7
-// have no row group, 256 B covering panels 2(v-4), 2(v-4)+1.  Every wave
-// issues Geometry<MT>::kLoadsPerStage instructions per stage.  The parts ride
-// between the MFMAs of the four k-steps, so the vector-memory pipe drains
-// while the matrix pipe is busy.
+// One chunk's int8 weight units and scales of the wave's two panels
+struct RawW {
+  u32x4 u[2][2];   // [panel t][unit j]: k = 32h + 16j + 0..15 of row r
+  uint32_t s[2];   // fp16 scale bits of block h, row r (low half)
+};
+
+// Wait until `w`'s loads have landed: at most N later loads outstanding.  The
+// registers are operands, so no use of them can be scheduled before the wait.
+template <int N>
+__device__ inline void wait_weights(RawW &w) {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%[n])"
+               : "+v"(w.u[0][0]), "+v"(w.u[0][1]), "+v"(w.u[1][0]), "+v"(w.u[1][1]), "+v"(w.s[0]),
+                 "+v"(w.s[1])
+               : [n] "n"(N));
+}
+
+// Per-wave load plan, fixed for the whole K loop.
 template <int MT>
-__device__ inline void issue_part(uint8_t *stage, int part, const f16 *__restrict__ A,
-                                  const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
-                                  uint32_t M, uint32_t K, uint32_t m0, uint32_t p0, uint32_t np,
-                                  uint32_t c, uint32_t wave, uint32_t lane) {
-  uint8_t *Ws = stage;
-  uint8_t *Ss = stage + kWBytes;
-  uint8_t *As = stage + kWBytes + kSBytes;
-  if (part < 2) {
-    uint32_t p = p0 + wave;
-    p = p < np ? p : np - 1;  // panels past N: valid bytes, results never stored
-    dma16(qs + panel_chunk_qs(K, p, kPanelRows, c) + part * 1024 + lane * 16,
-          Ws + wave * 2048 + part * 1024);
-  } else if (part == 2) {
-    // lane l fills physical chunk l%8 of row 8g + l/8 with the logical chunk
-    // that the swizzle stores there
+struct Plan {
+  desc_t wq, ws, wa, zero;  // weights, scales, activations, empty
+  uint32_t w_soff[2];       // byte offset of panel (2*wave + t) in the weights
+  uint32_t s_voff[2];       // per-lane byte offset of this lane's scale, panel t
+  uint32_t a_voff[MT];      // per-lane activation offsets of the wave's row groups
+  uint32_t nchunks;
+};
+
+// The vector-memory issues of k-step s for chunk c's A stage (into `slot`) and
+// chunk cw's weights (into `w`); chunks past the last one load zeros.
+template <int MT>
+__device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, uint32_t cw,
+                                   const Plan<MT> &p, uint32_t wave, uint32_t lane) {
+  const desc_t wa = c < p.nchunks ? p.wa : p.zero;
+  const bool live = cw < p.nchunks;
+  const desc_t wq = live ? p.wq : p.zero, ws = live ? p.ws : p.zero;
+  const uint32_t base = lds_addr(slot);
+  if (s == 0) {
 #pragma unroll
-    for (int g = (int)wave; g < 4 * MT; g += kWaves) {
-      const uint32_t row = g * 8 + (lane >> 3);
-      const uint32_t q = (lane & 7) ^ a_swz(row);
-      uint32_t m = m0 + row;
-      m = m < M ? m : M - 1;  // rows past M: valid bytes, results never stored
-      dma16(A + (size_t)m * K + c * kChunkK + q * 8, As + g * 1024);
-    }
+    for (int i = 0; i < MT / 2; ++i) dma16(wa, p.a_voff[i], c * 128, base + (wave + 4 * i) * 1024);
+  } else if (s == 1) {
+#pragma unroll
+    for (int i = MT / 2; i < MT; ++i) dma16(wa, p.a_voff[i], c * 128, base + (wave + 4 * i) * 1024);
+    vload16(w.u[0][0], wq, lane * 16, p.w_soff[0] + cw * 2048);
+  } else if (s == 2) {
+    vload16(w.u[0][1], wq, lane * 16, p.w_soff[0] + cw * 2048 + 1024);
+    vload16(w.u[1][0], wq, lane * 16, p.w_soff[1] + cw * 2048);
   } else {
-    if constexpr (MT == 1) {
-      if (wave >= 4 && lane < 16) {
-        const uint32_t t = (wave - 4) * 2 + (lane >> 3), q = lane & 7;
-        uint32_t pp = p0 + t;
-        pp = pp < np ? pp : np - 1;
-        dma16(sc + panel_chunk_sc(K, pp, kPanelRows, c) + q * 8, Ss + (wave - 4) * 256);
-      }
-    } else {
-      uint32_t p = p0 + wave;
-      p = p < np ? p : np - 1;
-      if (lane < 8) dma16(sc + panel_chunk_sc(K, p, kPanelRows, c) + lane * 8, Ss + wave * 128);
-    }
+    vload16(w.u[1][1], wq, lane * 16, p.w_soff[1] + cw * 2048 + 1024);
+    vload2(w.s[0], ws, p.s_voff[0], cw * 128);
+    vload2(w.s[1], ws, p.s_voff[1], cw * 128);
   }
 }
 
-template <int MT>
-__device__ inline void issue_stage(uint8_t *stage, const f16 *__restrict__ A,
-                                   const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
-                                   uint32_t M, uint32_t K, uint32_t m0, uint32_t p0, uint32_t np,
-                                   uint32_t c, uint32_t wave, uint32_t lane) {
-#pragma unroll
-  for (int part = 0; part < 4; ++part)
-    issue_part<MT>(stage, part, A, qs, sc, M, K, m0, p0, np, c, wave, lane);
-}
-
-// The MT activation fragments of k-step s from an A tile (swizzled rows).
+// The MT activation fragments of k-step s from an A stage (swizzled rows).
 template <int MT>
 __device__ inline void load_a_frags(const uint8_t *As, int s, uint32_t h, uint32_t r,
                                     f16x8 (&bf)[MT]) {
@@ -130,20 +204,79 @@ __device__ inline void load_a_frags(const uint8_t *As, int s, uint32_t h, uint32
     bf[i] = *reinterpret_cast<const f16x8 *>(As + (i * 32 + r) * 128 + phys);
 }
 
-// One 16-byte weight unit (half j of this wave's panel) of the chunk in
-// `stage`, dequantised into two k-steps.
-__device__ inline void dequant_unit(const uint8_t *stage, uint32_t wave, uint32_t lane, int j,
-                                    f16 s, f16x8 &lo, f16x8 &hi) {
-  const u32x4 u = *reinterpret_cast<const u32x4 *>(stage + wave * 2048 + j * 1024 + lane * 16);
-  dequant16(u, s, lo, hi);
+// The k-step-s fragment of panel t: half (s & 1) of unit s >> 1.
+__device__ inline f16x8 dequant_frag(const RawW &w, int t, int s) {
+  const u32x4 u = w.u[t][s >> 1];
+  const uint32_t b0 = (s & 1) ? u.z : u.x, b1 = (s & 1) ? u.w : u.y;
+  const f16 sc = __builtin_bit_cast(f16, (uint16_t)w.s[t]);
+  const f16x2 s2 = {sc, sc};
+  const f16x2 a0 = dequant_pair(b0, kSelLo, s2), a1 = dequant_pair(b0, kSelHi, s2);
+  const f16x2 a2 = dequant_pair(b1, kSelLo, s2), a3 = dequant_pair(b1, kSelHi, s2);
+  return (f16x8){a0.x, a0.y, a1.x, a1.y, a2.x, a2.y, a3.x, a3.y};
 }
 
-__device__ inline f16 panel_scale(const uint8_t *stage, uint32_t wave, uint32_t lane) {
-  return reinterpret_cast<const f16 *>(stage + kWBytes)[wave * 64 + lane];
+// sched_group_barrier masks
+constexpr int kSchedVALU = 0x002;
+constexpr int kSchedMFMA = 0x008;
+constexpr int kSchedVMEM = 0x020;
+constexpr int kSchedDSRead = 0x100;
+
+// Instruction order of one k-step: its LDS reads first (their latency hides
+// under this step's MFMAs), then each MFMA followed by up to three VALU ops
+// (the dequantisation, 24 per step) and a vector-memory issue.
+template <int MT>
+__device__ inline void schedule_step() {
+  __builtin_amdgcn_sched_group_barrier(kSchedDSRead, MT, 0);
+#pragma unroll
+  for (int i = 0; i < 2 * MT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedVALU, 24 / (2 * MT) + 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedVMEM, 1, 0);
+  }
+}
+
+// One chunk c.  On entry w holds chunk c's fragments except w[1][3] (made at
+// step 0 from `cur`, chunk c's weights), `af` holds chunk c's step-0
+// activation fragments, and `nxt` receives chunk c+1's weights (loaded WD-1
+// chunks ago; waited for here).  `ld` (the same
+// register set as `cur`, free after step 0) receives chunk c+WD's weights.
+template <int MT>
+__device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint32_t wave,
+                             uint32_t lane, uint32_t h, uint32_t r, f32x16 (&acc)[2][MT],
+                             f16x8 (&w)[2][4], f16x8 (&af)[MT], const RawW &cur, RawW &nxt,
+                             RawW &ld) {
+  using G = Geometry<MT>;
+  const uint8_t *At = smem + (c % NA) * G::kStage;
+  const uint8_t *An = smem + ((c + 1) % NA) * G::kStage;
+  uint8_t *Af = smem + ((c + NA - 1) % NA) * G::kStage;
+  wait_weights<G::kVmRaw>(nxt);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (s == 3) wait_then_barrier<G::kVmA>();  // chunk c+1's A stage is visible
+    f16x8 an[MT];
+    if (s < 3)
+      load_a_frags<MT>(At, s + 1, h, r, an);
+    else
+      load_a_frags<MT>(An, 0, h, r, an);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[0][s], af[i], acc[0][i], 0, 0, 0);
+    // panel 1's step s-1 fragment was consumed last step: refill it
+    w[1][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 1, (s + 3) & 3);
+#pragma unroll
+    for (int i = 0; i < MT; ++i)
+      acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[1][s], af[i], acc[1][i], 0, 0, 0);
+    w[0][s] = dequant_frag(nxt, 0, s);
+    issue_loads<MT>(s, Af, c + NA - 1, ld, c + WD, p, wave, lane);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) af[i] = an[i];
+    schedule_step<MT>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 template <int MT, int EPI>
-__global__ __launch_bounds__(512) void q8_gemm_kernel(const f16 *__restrict__ A,
+__global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
                                                       const uint8_t *__restrict__ qs,
                                                       const f16 *__restrict__ sc,
                                                       f16 *__restrict__ Cout,
@@ -151,7 +284,7 @@ __global__ __launch_bounds__(512) void q8_gemm_kernel(const f16 *__restrict__ A,
                                                       uint32_t N, uint32_t K, uint32_t tiles_m,
                                                       uint32_t tiles_n, uint32_t group_m) {
   using G = Geometry<MT>;
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[NSTAGES * G::kStage];
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[G::kLds];
 
   // ---- tile order: consecutive workgroups go to different XCDs (round-robin),
   // so renumber to give each XCD a contiguous run, then walk that run in
@@ -166,102 +299,125 @@ __global__ __launch_bounds__(512) void q8_gemm_kernel(const f16 *__restrict__ A,
   const uint32_t tm = first_m + (bid % per_group) % gm;
   const uint32_t tn = (bid % per_group) / gm;
 
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
   const uint32_t m0 = tm * 32 * MT, p0 = tn * kPanelsPerTile;
   const uint32_t np = N / kPanelRows, nchunks = K / kChunkK;
 
-  f32x16 acc[MT];
+  // ---- load plan.  Panels past N and rows past M are clamped to the last
+  // valid one: their bytes are read but their results are never stored.
+  Plan<MT> p;
+  p.wq = make_desc(qs, N * K);
+  p.ws = make_desc(sc, N * K / 16);
+  p.wa = make_desc(A, M * K * 2);
+  p.zero = make_desc(A, 0);
+  p.nchunks = nchunks;
 #pragma unroll
-  for (int i = 0; i < MT; ++i) acc[i] = (f32x16){};
-
-  // ---- software pipeline over a four-slot ring.  At iteration c: chunk c's
-  // activation fragments feed this iteration's MFMAs (its weights were
-  // dequantised during iteration c-1), chunk c+1's weights are dequantised
-  // between the MFMAs, chunk c+2 is in flight and chunk c+3 is issued, a part
-  // per k-step, into the slot chunk c-1 left (free once every wave passed
-  // this iteration's barrier).
-#pragma unroll
-  for (int st = 0; st < NSTAGES - 1; ++st)
-    if (st < (int)nchunks)
-      issue_stage<MT>(smem + st * G::kStage, A, qs, sc, M, K, m0, p0, np, st, wave, lane);
-  if (nchunks >= 3)
-    wait_vmcnt<2 * G::kLoadsPerStage>();
-  else
-    wait_vmcnt<0>();
-  __builtin_amdgcn_s_barrier();
-
-  f16x8 wcur[4], wnext[4];
-  {
-    const f16 s0 = panel_scale(smem, wave, lane);
-    dequant_unit(smem, wave, lane, 0, s0, wcur[0], wcur[1]);
-    dequant_unit(smem, wave, lane, 1, s0, wcur[2], wcur[3]);
+  for (int t = 0; t < 2; ++t) {
+    uint32_t pp = p0 + 2 * wave + t;
+    pp = pp < np ? pp : np - 1;
+    p.w_soff[t] = pp * kPanelRows * K;
+    p.s_voff[t] = pp * K * 2 + lane * 2;  // panel pp's chunk c scales at pp*K + 64c elements
   }
-  f16x8 bcur[MT], bnext[MT];
-  load_a_frags<MT>(smem + kWBytes + kSBytes, 0, h, r, bcur);
-
-  for (uint32_t c = 0; c < nchunks; ++c) {
-    if (c + 1 < nchunks) {
-      // chunk c+1 has landed once only chunk c+2's loads may be outstanding;
-      // the barrier publishes every wave's part and retires slot c-1
-      if (c + 2 < nchunks)
-        wait_vmcnt<G::kLoadsPerStage>();
-      else
-        wait_vmcnt<0>();
-      __builtin_amdgcn_s_barrier();
-    }
-    const bool refill = c + 3 < nchunks;  // chunk c+3's DMA rides between the steps
-    uint8_t *Rs = smem + ((c + 3) % NSTAGES) * G::kStage;
-    // Branch-free compute region; on the last chunk the "next" slot holds
-    // stale, in-bounds bytes whose dequantised values are never used.
-    const uint8_t *As = smem + (c % NSTAGES) * G::kStage + kWBytes + kSBytes;
-    const uint8_t *Wn = smem + ((c + 1) % NSTAGES) * G::kStage;
-    const uint8_t *An = Wn + kWBytes + kSBytes;
-    const f16 snext = panel_scale(Wn, wave, lane);
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      if (s < 3)
-        load_a_frags<MT>(As, s + 1, h, r, bnext);
-      else
-        load_a_frags<MT>(An, 0, h, r, bnext);
-      if (s == 1) dequant_unit(Wn, wave, lane, 0, snext, wnext[0], wnext[1]);
-      if (s == 3) dequant_unit(Wn, wave, lane, 1, snext, wnext[2], wnext[3]);
-#pragma unroll
-      for (int i = 0; i < MT; ++i)
-        acc[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wcur[s], bcur[i], acc[i], 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < MT; ++i) bcur[i] = bnext[i];
-      if (refill) issue_part<MT>(Rs, s, A, qs, sc, M, K, m0, p0, np, c + 3, wave, lane);
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) wcur[s] = wnext[s];
-  }
-
-  // ---- epilogue: lane holds D[n][m] for m = l%32, n = 8g + 4(l/32) + (0..3)
-  const uint32_t nb = (p0 + wave) * kPanelRows;
-  if (nb >= N) return;
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
-    const uint32_t m = m0 + i * 32 + r;
-    if (m >= M) continue;
+    const uint32_t row = (wave + 4 * i) * 8 + (lane >> 3);
+    const uint32_t q = (lane & 7) ^ a_swz(row);
+    uint32_t m = m0 + row;
+    m = m < M ? m : M - 1;
+    p.a_voff[i] = m * K * 2 + q * 16;
+  }
+
+  f32x16 acc[2][MT];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const uint32_t n = nb + g * 8 + h * 4;
-      float v[4] = {acc[i][g * 4 + 0], acc[i][g * 4 + 1], acc[i][g * 4 + 2], acc[i][g * 4 + 3]};
-      if constexpr (EPI != MADI_EPI_NONE) {
-        const f32x4 b4 = *reinterpret_cast<const f32x4 *>(bias + n);
-        v[0] += b4.x;
-        v[1] += b4.y;
-        v[2] += b4.z;
-        v[3] += b4.w;
-        if constexpr (EPI == MADI_EPI_BIAS_GELU) {
+  for (int t = 0; t < 2; ++t)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
-        }
-      }
-      const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-      *reinterpret_cast<f16x4 *>(Cout + (size_t)m * N + n) = o;
+    for (int i = 0; i < MT; ++i) acc[t][i] = (f32x16){};
+
+  // ---- prologue: the loads the steady state would have issued before chunk 0
+  // (virtual chunks -WD .. -1), in the same order, so the loop's vmcnt waits
+  // hold from the first chunk on.  Virtual chunk j loads A stage j+NA-1 (a
+  // negative, i.e. wrapped and out-of-range, stage loads zeros into a slot
+  // nothing reads) and weights j+WD; register set k receives chunks k, k+WD, ...
+  RawW r0, r1, r2, r3;
+  static_assert(WD == 4, "the loop below rotates four weight register sets");
+  static_assert(NA >= 3 && NA <= WD + 1, "the prologue covers the first NA-1 stages");
+#pragma unroll
+  for (int j = -WD; j < 0; ++j) {
+    const uint32_t ca = (uint32_t)(j + NA - 1);
+    uint8_t *slot = smem + (uint32_t)((j + NA - 1 + NA) % NA) * G::kStage;
+    RawW &rw = j == -4 ? r0 : j == -3 ? r1 : j == -2 ? r2 : r3;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) issue_loads<MT>(st, slot, ca, rw, (uint32_t)(j + WD), p, wave, lane);
+  }
+  // chunk 0's weights and A stage, then its fragments
+  wait_then_barrier<G::kVmPrologue>();
+  wait_weights<G::kVmPrologue>(r0);
+  f16x8 w[2][4], af[MT];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) w[0][s] = dequant_frag(r0, 0, s);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) w[1][s] = dequant_frag(r0, 1, s);
+  load_a_frags<MT>(smem, 0, h, r, af);
+
+  // ---- main loop: four chunks per trip (the weight register sets rotate)
+  const uint32_t cpad = (nchunks + WD - 1) / WD * WD;
+  for (uint32_t c = 0; c < cpad; c += 4) {
+    chunk<MT>(smem, p, c + 0, wave, lane, h, r, acc, w, af, r0, r1, r0);
+    chunk<MT>(smem, p, c + 1, wave, lane, h, r, acc, w, af, r1, r2, r1);
+    chunk<MT>(smem, p, c + 2, wave, lane, h, r, acc, w, af, r2, r3, r2);
+    chunk<MT>(smem, p, c + 3, wave, lane, h, r, acc, w, af, r3, r0, r3);
+  }
+
+  // ---- epilogue.  Lane (h, r) holds D[n][m] for m = 32i + r and
+  // n = 32(2w + t) + 8g + 4h + e (acc[t][i][4g + e]).  Every wave must finish
+  // reading the ring before it becomes the C tile.
+  wait_then_barrier<0>();
+  uint8_t *Ct = smem;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const uint32_t nl = (2 * wave + t) * kPanelRows;  // tile-local column of the panel
+    f32x4 b4[4];
+    if constexpr (EPI != MADI_EPI_NONE) {
+      uint32_t p = p0 + 2 * wave + t;
+      p = p < np ? p : np - 1;  // clamped panels: bias read in bounds, result never stored
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        b4[g] = *reinterpret_cast<const f32x4 *>(bias + p * kPanelRows + g * 8 + h * 4);
     }
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float v[4] = {acc[t][i][g * 4 + 0], acc[t][i][g * 4 + 1], acc[t][i][g * 4 + 2],
+                      acc[t][i][g * 4 + 3]};
+        if constexpr (EPI != MADI_EPI_NONE) {
+          v[0] += b4[g].x;
+          v[1] += b4[g].y;
+          v[2] += b4[g].z;
+          v[3] += b4[g].w;
+          if constexpr (EPI == MADI_EPI_BIAS_GELU) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+          }
+        }
+        const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+        *reinterpret_cast<f16x4 *>(Ct + (i * 32 + r) * kCStride + (nl + g * 8 + h * 4) * 2) = o;
+      }
+    }
+  }
+  __syncthreads();
+  // wave w stores tile rows [8*MT*w, 8*MT*(w+1)), two rows (512 B each) per
+  // instruction: lane (h, r) writes 16 bytes of row 2j + h at column 8r
+  const uint32_t n = p0 * kPanelRows + r * 8;
+  if (n >= N) return;
+#pragma unroll
+  for (int j = 0; j < 4 * MT; ++j) {
+    const uint32_t row = wave * 8 * MT + 2 * j + h;
+    const uint32_t m = m0 + row;
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * kCStride + r * 16);
+    if (m < M) *reinterpret_cast<u32x4 *>(Cout + (size_t)m * N + n) = v;
   }
 }
 
@@ -297,9 +453,13 @@ extern "C" int madi_q8_gemm(const void *a, const void *qs, const void *scales, v
     return fail(MADI_ERR_ARG, "madi_q8_gemm: the residual epilogue exists for the GEMV only");
   if (m == 0 || n == 0 || k == 0 || n % kPanelRows || k % kChunkK)
     return fail(MADI_ERR_SHAPE, "madi_q8_gemm: m=%u n=%u k=%u (need n %% 32 == 0, k %% 64 == 0)", m, n, k);
-  if (!aligned(a, 16) || !aligned(qs, 16) || !aligned(scales, 16) || !aligned(c, 8) ||
+  // buffer offsets are 32-bit (and buffer sizes below 2 GiB): the operands
+  // A (m*k*2 bytes) and W (n*k bytes) must stay below 2 GiB
+  if ((uint64_t)m * k * 2 >= (1ull << 31) || (uint64_t)n * k >= (1ull << 31))
+    return fail(MADI_ERR_SHAPE, "madi_q8_gemm: m=%u n=%u k=%u exceeds the 2 GiB operand limit", m, n, k);
+  if (!aligned(a, 16) || !aligned(qs, 16) || !aligned(scales, 16) || !aligned(c, 16) ||
       (bias && !aligned(bias, 16)))
-    return fail(MADI_ERR_ALIGN, "madi_q8_gemm: a/qs/scales/bias need 16-byte, c 8-byte alignment");
+    return fail(MADI_ERR_ALIGN, "madi_q8_gemm: a/qs/scales/c/bias need 16-byte alignment");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_gemm: madi_init has not succeeded");
   const f16 *A = static_cast<const f16 *>(a);
   const uint8_t *Q = static_cast<const uint8_t *>(qs);
