@@ -3,31 +3,37 @@
 // Replaces gemv_q8 / _bias / _bias_gelu / _bias_res / _qkv and logit_gemv_q8
 // (engine/metal/kernels/graph_helpers.metal:320-558).  The reference runs one
 // 32-lane simdgroup per output row reading char4 + float4; here a 256-thread
-// workgroup streams two 32-row panels of the panel layout: every wave64 load
-// instruction moves one contiguous KiB (16 bytes per lane, 128-bit loads) and
-// each lane (h, r) accumulates the 32-weight block of row r, K-half h, of each
-// 64-wide chunk.  The four waves split K; the two K-halves meet with one
-// cross-lane shuffle and the four waves through LDS.
+// workgroup owns one 32-row panel of the panel layout and its four waves split
+// K.  Every wave64 load instruction moves one contiguous KiB (16 bytes per
+// lane, lane (h, r) receiving 16 weights of row r in quantisation block h),
+// issued as a buffer load with the panel/chunk offset in an SGPR.  Each wave
+// streams its K range through a two-chunk window (use chunk c, refill with
+// chunk c+2).  The kernel keeps to 72 VGPRs (seven waves per SIMD, seven
+// workgroups per CU), so every workgroup of the 51866-row vocab matrix (1621
+// panels) is resident from the start.
 //
-// Activations are staged once per workgroup in LDS as f32 and read as broadcast
-// 128-bit LDS loads shared by both panels.  The stored bytes are u = q + 128:
-// per block the lane forms sum_i x_i * u_i - 128 * sum_i x_i (the x sums are
-// staged with x), then multiplies by the block's scale, the same
-// (partial * scale) structure as the reference's kernels.
+// The activation vector is loaded before the weights, staged once per
+// workgroup in LDS with its 32-wide block sums and read back as broadcast
+// 128-bit LDS loads.  v_perm_b32 turns two stored bytes u = q + 128 into the
+// exact fp16 pair 1024 + u (one VALU op per two weights); fp16 activations
+// accumulate x * (1024 + u) with v_dot2_f32_f16, fp32 activations with FMA,
+// and each block subtracts 1152 * sum(x) to leave sum(x * q).  Per
+// quantisation block the lane multiplies its partial by the block's scale, the
+// same (partial * scale) structure as the reference's kernels; the two
+// K-halves meet by a cross-lane shuffle and the four waves through LDS.
 #include "common.h"
 
 using namespace madi;
 
 namespace {
 
-#ifndef MADI_GEMV_PPW
-#define MADI_GEMV_PPW 1
-#endif
-#ifndef MADI_GEMV_UNROLL
-#define MADI_GEMV_UNROLL 5
-#endif
-constexpr int kPanelsPerWG = MADI_GEMV_PPW;
-constexpr int kUnroll = MADI_GEMV_UNROLL;  // chunks whose loads are in flight together
+constexpr int kWaves = 4;          // K quarters per panel
+// Chunks in flight per wave, a sliding window: two keeps ~26 MB of the vocab
+// matrix in flight across the GPU, enough to cover HBM latency, while the
+// texture queues stay short enough that the activation vector (loaded first)
+// is not stuck behind a flood of weight requests; deeper windows measured
+// slower (the waves then sit blocked on issue and compute in one late burst).
+constexpr int kWin = 2;
 constexpr uint32_t kMaxK = 12288;
 
 enum GemvMode { kPlain = 0, kBias = 1, kBiasGelu = 2, kBiasRes = 3, kQkv = 4 };
@@ -45,118 +51,162 @@ struct GemvArgs {
   const uint32_t *pos;
 };
 
-__device__ inline float byte_f(uint32_t w, int i) { return (float)((w >> (8 * i)) & 0xffu); }
+// LDS bytes: x (K elements of XT), its K/32 block sums (fp32), the wave partials
+template <typename XT>
+constexpr size_t lds_bytes(uint32_t k) {
+  return (size_t)k * sizeof(XT) + (size_t)(k / 32) * 4 + kWaves * 32 * 4;
+}
 
-struct Batch {
-  u32x4 w[kUnroll][kPanelsPerWG][2];
-  f16 s[kUnroll][kPanelsPerWG];
+// One chunk's loads for a lane: its two 16-byte units and its block's scale.
+struct ChunkW {
+  u32x4 w[2];
+  uint32_t s;
 };
 
-// Issue the loads of chunks [c, min(c + kUnroll, c1)) of the workgroup's panels.
-__device__ inline void load_batch(Batch &b, const GemvArgs &a, uint32_t K, uint32_t c,
-                                  uint32_t c1, uint32_t p0, const uint32_t *R, const bool *live,
-                                  uint32_t h, uint32_t r) {
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ inline rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
+}
+
+// Issue chunk c of panel p (R rows) with buffer loads: the panel and chunk
+// offsets are uniform (SGPR) and the lane offsets fixed, so the loads need no
+// per-load address arithmetic.
+__device__ inline void load_chunk(ChunkW &b, rsrc_t wq, rsrc_t ws, uint32_t K, uint32_t c,
+                                  uint32_t p, uint32_t R, uint32_t w_voff, uint32_t s_voff) {
+  const uint32_t so = (uint32_t)panel_chunk_qs(K, p, R, c);
+  b.w[0] = __builtin_amdgcn_raw_buffer_load_b128(wq, w_voff, so, 0);
+  b.w[1] = __builtin_amdgcn_raw_buffer_load_b128(wq, w_voff + 2 * R * 16, so, 0);
+  b.s = __builtin_amdgcn_raw_buffer_load_b16(ws, s_voff, (uint32_t)panel_chunk_sc(K, p, R, c) * 2, 0);
+}
+
+// sum_i x[i] * (1024 + u_i) over one 16-byte unit of biased bytes u = q + 128,
+// fp16 activations: v_perm_b32 turns two bytes into the exact fp16 pair
+// (1024 + u0, 1024 + u1) and v_dot2_f32_f16 accumulates both products in fp32
+// (each product is exact).  The caller removes 1152 * sum(x).
+__device__ inline float unit_dot(const u32x4 &w, const f16 *x16, float part) {
+  const f16x8 xa = *reinterpret_cast<const f16x8 *>(x16);
+  const f16x8 xb = *reinterpret_cast<const f16x8 *>(x16 + 8);
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-  for (int u = 0; u < kUnroll; ++u)
+  for (int d = 0; d < 4; ++d) {
+    const f16x8 &xv = d < 2 ? xa : xb;
+    const int e = (d & 1) * 4;
+    const f16x2 u01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, wd[d], kSelLo));
+    const f16x2 u23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, wd[d], kSelHi));
+    part = __builtin_amdgcn_fdot2(u01, (f16x2){xv[e], xv[e + 1]}, part, false);
+    part = __builtin_amdgcn_fdot2(u23, (f16x2){xv[e + 2], xv[e + 3]}, part, false);
+  }
+  return part;
+}
+
+// The same sum for fp32 activations: v_fma_mix_f32 multiplies the fp32 x by
+// the fp16 value 1024 + u straight out of the perm (one rounding per step).
+__device__ inline float unit_dot(const u32x4 &w, const float *x32, float part) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
-    for (int t = 0; t < kPanelsPerWG; ++t) {
-      if (c + u < c1 && live[t]) {
-        const uint32_t p = p0 + t, Rt = R[t];
-        const uint8_t *blk = a.qs + panel_chunk_qs(K, p, Rt, c + u);
-        b.w[u][t][0] = *reinterpret_cast<const u32x4 *>(blk + (h * Rt + r) * 16);
-        b.w[u][t][1] = *reinterpret_cast<const u32x4 *>(blk + ((2 + h) * Rt + r) * 16);
-        b.s[u][t] = a.sc[panel_chunk_sc(K, p, Rt, c + u) + h * Rt + r];
-      }
-    }
+  for (int d = 0; d < 4; ++d) {
+    const f32x4 xv = *reinterpret_cast<const f32x4 *>(x32 + 4 * d);
+    const f16x2 u01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, wd[d], kSelLo));
+    const f16x2 u23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, wd[d], kSelHi));
+    part = __builtin_fmaf(xv.x, (float)u01.x, part);
+    part = __builtin_fmaf(xv.y, (float)u01.y, part);
+    part = __builtin_fmaf(xv.z, (float)u23.x, part);
+    part = __builtin_fmaf(xv.w, (float)u23.y, part);
+  }
+  return part;
+}
+
+// acc += scale * (sum_k x[k] q[k]) over the lane's quantisation block of chunk
+// c; q = (1024 + u) - 1152, so the block subtracts 1152 * (sum of its 32 x).
+template <typename XT>
+__device__ inline void accumulate(const ChunkW &b, uint32_t c, const XT *xs, const float *xsum,
+                                  uint32_t h, float &acc) {
+  const uint32_t k0 = c * kChunkK + h * 32;  // the lane's 32-wide block
+  float part = unit_dot(b.w[0], xs + k0, 0.0f);
+  part = unit_dot(b.w[1], xs + k0 + 16, part);
+  part = __builtin_fmaf(-1152.0f, xsum[k0 >> 5], part);
+  acc = __builtin_fmaf(part, (float)__builtin_bit_cast(f16, (uint16_t)b.s), acc);
 }
 
 template <typename XT, int MODE>
-__global__ __launch_bounds__(256) void q8_gemv_kernel(GemvArgs a) {
-  extern __shared__ float smem[];
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q8_gemv_kernel(
+    GemvArgs a) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr bool kF16 = sizeof(XT) == 2;
   const uint32_t K = a.k, C = K / kChunkK;
-  float *xs = smem;                 // [K]
-  float *xsum = smem + K;           // [C][2]: sum of each 32-wide half-chunk
-  float *red = xsum + 2 * C;        // [4 waves][kPanelsPerWG * 32]
+  XT *xs = reinterpret_cast<XT *>(smem);                        // [K]
+  float *xsum = reinterpret_cast<float *>(smem + K * sizeof(XT));  // [K/32]
+  float *red = reinterpret_cast<float *>(smem + lds_bytes<XT>(K) - kWaves * 32 * 4);  // [4][32]
 
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
-  const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
-  const uint32_t p0 = blockIdx.x * kPanelsPerWG;
+  const uint32_t p = blockIdx.x;
+  const uint32_t R = panel_rows(a.n, p);
+  const bool live = r < R;
+  const uint32_t c0 = (wave * C) / kWaves, c1 = ((wave + 1) * C) / kWaves;
 
-  uint32_t R[kPanelsPerWG];
-  bool live[kPanelsPerWG];
+  // ---- x: load first (16 bytes per thread and piece), then the weights.
+  // Lanes past a partial panel's last row read row R-1 (in bounds; their sums
+  // are never stored).
+  const uint32_t pieces = K * sizeof(XT) / 16;
+  const rsrc_t xr = make_rsrc(a.x, K * sizeof(XT));
+  u32x4 xv0 = {}, xv1 = {};
+  const uint32_t i0 = threadIdx.x, i1 = threadIdx.x + 256;
+  if (i0 < pieces) xv0 = __builtin_amdgcn_raw_buffer_load_b128(xr, i0 * 16, 0, 0);
+  if (i1 < pieces) xv1 = __builtin_amdgcn_raw_buffer_load_b128(xr, i1 * 16, 0, 0);
+
+  const rsrc_t wq = make_rsrc(a.qs, a.n * K), ws = make_rsrc(a.sc, a.n * (K / 32) * 2);
+  const uint32_t rr = live ? r : R - 1;
+  const uint32_t w_voff = (h * R + rr) * 16, s_voff = (h * R + rr) * 2;
+  // the first kWin chunks of this wave's range go in flight behind x
+  ChunkW win[kWin];
 #pragma unroll
-  for (int t = 0; t < kPanelsPerWG; ++t) {
-    const uint32_t p = p0 + t;
-    R[t] = p < np ? panel_rows(a.n, p) : 0;
-    live[t] = r < R[t];
-  }
-  const uint32_t c0 = (wave * C) / 4, c1 = ((wave + 1) * C) / 4;
+  for (int k = 0; k < kWin; ++k)
+    if (c0 + k < c1) load_chunk(win[k], wq, ws, K, c0 + k, p, R, w_voff, s_voff);
 
-  // The first weight batch does not depend on x: put it in flight before the
-  // x prologue so the activation staging hides under HBM latency.
-  Batch b;
-  load_batch(b, a, K, c0, c1, p0, R, live, h, r);
-
-  // Stage x as f32; each 32-lane group also reduces one 32-wide block sum.
-  const XT *x = static_cast<const XT *>(a.x);
-  for (uint32_t i = threadIdx.x; i < K; i += 256) {
-    const float v = (float)x[i];
-    xs[i] = v;
-    float sum = v;
+  // stage x and its 32-wide block sums (in fp32; the pieces of one block sit in
+  // 32 * sizeof(XT) / 16 adjacent lanes)
+  constexpr uint32_t kPer = 32 * sizeof(XT) / 16;  // 16-byte pieces per block
+  for (uint32_t i = threadIdx.x; i < pieces; i += 256) {
+    const u32x4 v =
+        i == i0 ? xv0 : (i == i1 ? xv1 : __builtin_amdgcn_raw_buffer_load_b128(xr, i * 16, 0, 0));
+    reinterpret_cast<u32x4 *>(xs)[i] = v;
+    float sp;
+    if constexpr (kF16) {
+      const f16x8 f = __builtin_bit_cast(f16x8, v);
+      sp = (((float)f[0] + (float)f[1]) + ((float)f[2] + (float)f[3])) +
+           (((float)f[4] + (float)f[5]) + ((float)f[6] + (float)f[7]));
+    } else {
+      const f32x4 f = __builtin_bit_cast(f32x4, v);
+      sp = (f.x + f.y) + (f.z + f.w);
+    }
 #pragma unroll
-    for (int off = 16; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, 32);
-    if ((i & 31) == 0) xsum[i >> 5] = sum;
+    for (uint32_t off = 1; off < kPer; off <<= 1) sp += __shfl_xor(sp, off, kPer);
+    if ((i & (kPer - 1)) == 0) xsum[i / kPer] = sp;
   }
   __syncthreads();
 
-  float acc[kPanelsPerWG] = {};
-  for (uint32_t c = c0; c < c1; c += kUnroll) {
-    if (c != c0) load_batch(b, a, K, c, c1, p0, R, live, h, r);
+  // stream the range through the kWin-chunk window: use chunk c, refill its
+  // registers with chunk c + kWin
+  float acc = 0.0f;
+#pragma unroll 1
+  for (uint32_t c = c0; c < c1; c += kWin) {
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (c + u >= c1) break;
-      const f32x4 *xv = reinterpret_cast<const f32x4 *>(xs + (c + u) * kChunkK + h * 32);
-      f32x4 xr[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) xr[q] = xv[q];
-      const float xsm = xsum[(c + u) * 2 + h];
-#pragma unroll
-      for (int t = 0; t < kPanelsPerWG; ++t) {
-        if (!live[t]) continue;
-        float part = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const u32x4 ww = b.w[u][t][j];
-          const uint32_t wd[4] = {ww.x, ww.y, ww.z, ww.w};
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const f32x4 xq = xr[j * 4 + d];
-            part = __builtin_fmaf(xq.x, byte_f(wd[d], 0), part);
-            part = __builtin_fmaf(xq.y, byte_f(wd[d], 1), part);
-            part = __builtin_fmaf(xq.z, byte_f(wd[d], 2), part);
-            part = __builtin_fmaf(xq.w, byte_f(wd[d], 3), part);
-          }
-        }
-        part = __builtin_fmaf(-128.0f, xsm, part);
-        acc[t] = __builtin_fmaf(part, (float)b.s[u][t], acc[t]);
+    for (int k = 0; k < kWin; ++k) {
+      if (c + k < c1) {
+        accumulate<XT>(win[k], c + k, xs, xsum, h, acc);
+        if (c + k + kWin < c1) load_chunk(win[k], wq, ws, K, c + k + kWin, p, R, w_voff, s_voff);
       }
     }
   }
 
-#pragma unroll
-  for (int t = 0; t < kPanelsPerWG; ++t) {
-    acc[t] += __shfl_xor(acc[t], 32);
-    if (h == 0) red[wave * (kPanelsPerWG * 32) + t * 32 + r] = acc[t];
-  }
+  acc += __shfl_xor(acc, 32);
+  if (h == 0) red[wave * 32 + r] = acc;
   __syncthreads();
-  if (threadIdx.x >= kPanelsPerWG * 32) return;
-  const uint32_t t = threadIdx.x / 32, rr = threadIdx.x % 32;
-  if (p0 + t >= np || rr >= panel_rows(a.n, p0 + t)) return;
-  const uint32_t stride = kPanelsPerWG * 32;
-  const float v = red[threadIdx.x] + red[stride + threadIdx.x] + red[2 * stride + threadIdx.x] +
-                  red[3 * stride + threadIdx.x];
-  const uint32_t nrow = (p0 + t) * kPanelRows + rr;
+  if (threadIdx.x >= R) return;
+  const float v = red[threadIdx.x] + red[32 + threadIdx.x] + red[64 + threadIdx.x] + red[96 + threadIdx.x];
+  const uint32_t nrow = p * kPanelRows + threadIdx.x;
   if constexpr (MODE == kPlain) {
     a.out[nrow] = v;
   } else if constexpr (MODE == kBias) {
@@ -184,12 +234,11 @@ int launch(const char *what, const GemvArgs &a) {
   if (a.n == 0 || a.k == 0 || a.k % kChunkK)
     return fail(MADI_ERR_SHAPE, "%s: n=%u k=%u (need n > 0, k a positive multiple of 64)", what, a.n, a.k);
   if (a.k > kMaxK) return fail(MADI_ERR_SHAPE, "%s: k=%u exceeds %u", what, a.k, kMaxK);
-  if (!aligned(a.qs, 16) || !aligned(a.sc, 2) || !aligned(a.x, sizeof(XT)))
-    return fail(MADI_ERR_ALIGN, "%s: qs needs 16-byte alignment", what);
+  if (!aligned(a.qs, 16) || !aligned(a.sc, 2) || !aligned(a.x, 16))
+    return fail(MADI_ERR_ALIGN, "%s: qs and x need 16-byte alignment", what);
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);
-  const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
-  const uint32_t grid = (np + kPanelsPerWG - 1) / kPanelsPerWG;
-  const size_t lds = (a.k + 2 * (a.k / kChunkK) + 4 * kPanelsPerWG * 32) * sizeof(float);
+  const uint32_t grid = (a.n + kPanelRows - 1) / kPanelRows;
+  const size_t lds = lds_bytes<XT>(a.k);
   hipLaunchKernelGGL((q8_gemv_kernel<XT, MODE>), dim3(grid), dim3(256), lds, stream(), a);
   return check_launch(what);
 }
