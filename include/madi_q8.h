@@ -161,6 +161,17 @@ int madi_q8_logit_gemv(float *logits, const void *qs, const void *scales, const 
 int madi_q8_gemv_f16x(float *out, const void *x_f16, const void *qs, const void *scales,
                       const float *bias, uint32_t n, uint32_t k, int epilogue);
 
+/* Batched / skinny projection: out[M][N] (f32) = in[M][K] (f32) . deq(W)^T for
+ * a few token rows (the batched-decode GEMV; any M, 32 rows per pass over W).
+ * Replaces pproj (engine/metal/decoder.zig:427-432: kDeq + kCvt32 +
+ * matmulF16Batched + kCvt16) and the per-slot proj calls of the batched
+ * decode (decoder.zig:337-341) with one fused kernel: activations rounded to
+ * f16 and weights to fp16_rne(q * s) as that pipeline does, fp32
+ * accumulation, f32 result (the pipeline's f16 output staging is not
+ * repeated).  in must be 16-byte aligned; out may not alias in. */
+int madi_q8_pproj(float *out, const float *in, const void *qs, const void *scales,
+                  uint32_t m, uint32_t n, uint32_t k);
+
 /* Q8 embedding rows from the panel layout (the tied tok_emb the logit GEMV
  * reads): out[d] = f32(q) * f32(s) for row *tok_ptr (gpu_emb_lookup_q8,
  * graph_helpers.metal:370-383) or row tokens[*pos_ptr]

@@ -51,6 +51,7 @@ SIGNATURES = {
     "madi_q8_gemv_qkv": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _U32]),
     "madi_q8_logit_gemv": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_gemv_f16x": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _I]),
+    "madi_q8_pproj": (_I, [_P, _P, _P, _P, _U32, _U32, _U32]),
     "madi_q8_emb_lookup": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_emb_lookup_indirect": (_I, [_P, _P, _P, _P, _P, _U32, _U32]),
 }

@@ -146,6 +146,13 @@ def kGemvQ8BiasEpi(f: str, out, x, w: Q8, bias, n: int, k: int) -> None:
     call(name, ptr(out), ptr(x), w.qs, w.scales, ptr(bias), n, k)
 
 
+def pproj(in_f32, w: Q8, out_f32, M: int, N: int, Kk: int) -> None:
+    """decoder.zig:427-432 (pproj: kDeq + kCvt32 + matmulF16Batched + kCvt16)
+    as one fused kernel; also serves proj (decoder.zig:337-341) straight from
+    the Q8 weights.  in_f32 [M][Kk] -> out_f32 [M][N]."""
+    call("madi_q8_pproj", ptr(out_f32), ptr(in_f32), w.qs, w.scales, M, N, Kk)
+
+
 def kQkv(q_out, x, w: Q8, qb, vb, kc, vc, pos, d: int = D) -> None:
     """decoder.zig:169-174 (gemv_q8_qkv); pos is a device u32."""
     call("madi_q8_gemv_qkv", ptr(q_out), ptr(x), w.qs, w.scales, ptr(qb), ptr(vb), ptr(kc),
@@ -177,7 +184,7 @@ def gemv_f16x(out, x16, w: Q8, n: int, k: int, bias=None, epilogue: int = EPI_NO
 __all__ = [
     "D", "MLP", "VOCAB", "ENC_SEQ", "Q8", "init", "sync", "repack_host", "unpack_host",
     "upload_q8", "upload_q8_device_repack", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias",
-    "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "kQkv", "kLogitGemv", "embLookup",
+    "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "pproj", "kQkv", "kLogitGemv", "embLookup",
     "embLookupIndirect", "gemv_f16x", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU",
     "EPI_BIAS_RES",
 ]

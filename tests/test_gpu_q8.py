@@ -277,3 +277,55 @@ def test_emb_lookup_rows(q):
     q.embLookupIndirect(out, w.qs, w.scales, toks, pos, n, k)
     q.sync()
     assert np.array_equal(out.cpu().numpy(), O.emb_row_q8(qs, sc, 51864))
+
+
+# ------------------------------------------------------------------ batched / skinny projection
+def _pproj(q, x, qs, sc):
+    m, k = x.shape
+    n = qs.shape[0]
+    w = q.upload_q8(qs, sc)
+    out = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda")
+    q.pproj(dev(x), w, out, m, n, k)
+    q.sync()
+    return out.cpu().numpy()
+
+
+def staged_ok(c, x, qs, sc):
+    """Element-wise: pproj must equal sum_k f16(x_k) * fp16_rne(q_k s_k) (the
+    f16 staging of decoder.zig:427-432) up to fp32 accumulation error
+    (K * 2^-24 * sum|x16||w16|); it stores f32, so no output rounding."""
+    x16 = O.f32_to_f16(x).astype(np.float64)
+    w16 = O.dequant_q8_f16(qs, sc).astype(np.float64)  # [K][N]
+    exact = x16 @ w16
+    bound = x.shape[1] * 2.0**-24 * (np.abs(x16) @ np.abs(w16)) + 2.0**-40
+    return bool(np.all(np.abs(c.astype(np.float64) - exact) <= bound * 1.001))
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (1, 3840, 1280), (2, 3840, 1280), (8, 5120, 1280), (16, 1280, 5120),
+    (8, 51866, 1280),    # batched vocab logits, tail panel of 26 rows
+    (32, 1280, 1280), (33, 3840, 1280), (70, 1280, 5120), (5, 40, 64),
+])
+def test_pproj_parity(q, m, n, k):
+    say(f"pproj m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 131 + n + k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    qs, sc = synth.q8_weight(rng, n, k)
+    c = _pproj(q, x, qs, sc)
+    assert np.all(np.isfinite(c))
+    ref = O.q8_proj(x, qs, sc, threads=8)   # test_batchproj.zig:72-78, f32 throughout
+    assert normwise(c, ref) <= TOL, normwise(c, ref)
+    assert staged_ok(c, x, qs, sc)
+
+
+def test_pproj_one_hot_is_dequant(q):
+    """x = one-hot rows: out[m][n] = fp16_rne(q s) of column k_m, bit-exact."""
+    n, k = 96, 128
+    rng = np.random.default_rng(17)
+    qs, sc = synth.q8_weight(rng, n, k)
+    ks = np.array([0, 1, 31, 32, 63, 64, 100, 127])
+    x = np.zeros((len(ks), k), np.float32)
+    x[np.arange(len(ks)), ks] = 1.0
+    c = _pproj(q, x, qs, sc)
+    ref = O.dequant_q8_f16(qs, sc)[ks].astype(np.float32)  # [len(ks)][N]
+    assert np.array_equal(c, ref)
