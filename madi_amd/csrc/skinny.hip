@@ -12,24 +12,26 @@
 // one rounding the pipeline adds after the product, dropped: it only moves
 // the result away from the fp32 reference of test_batchproj.zig:72-78).
 //
-// Workgroup: one 32-row weight panel x one slice of 32 activation rows, four
-// waves splitting K like the GEMV.  Per 64-wide K chunk a wave loads the
-// panel's two 16-byte units per lane (lane (h, r): row r's 32 weights of
-// quantisation block h) and its scale, plus 32 f32 activations per lane (lane
-// (h, c): row c of the slice, the same 32 k), converts both to fp16 fragments
-// and runs four v_mfma_f32_32x32x16_f16 with the weight as the A operand (rows
-// n) and the activations as B (columns m).  K order of step s: k = 32h + 8s +
-// e for both operands, as in the GEMM.  Activation rows past M load as zeros
-// (their lanes' offsets fall outside the buffer resource), so small M costs
-// no extra memory traffic.  Each wave keeps a two-chunk window in flight; the
-// four K partial tiles meet in LDS and every wave stores one quarter.
+// Workgroup: P weight panels (32 rows each; P = 4 for the 51866-row vocab
+// matrix, 1 otherwise) x one slice of 32 activation rows, KW waves splitting
+// K (8 for single panels, 4 for panel groups).  Per 64-wide K chunk a wave
+// loads each panel's two 16-byte units per lane (lane (h, r): row r's 32
+// weights of quantisation block h) and scale, and the slice's 32 x 64 f32
+// activations with coalesced loads (each instruction: four whole 256-byte row
+// segments), rounds them to f16 into its own LDS tile and reads them back as
+// MFMA fragments (lane (h, c): row c, the same 32 k).  Four
+// v_mfma_f32_32x32x16_f16 per panel and chunk, with the weight as the A operand
+// (rows n) and the activations as B (columns m); K order of step s: k = 32h +
+// 8s + e for both operands, as in the GEMM.  Activation rows past M load as
+// zeros (outside the buffer resource), so small M costs no extra memory
+// traffic.  Each wave keeps a two-chunk window in flight; the K partial tiles
+// meet in LDS and four waves store one quarter each.
 #include "common.h"
 
 using namespace madi;
 
 namespace {
 
-constexpr int kWaves = 4;   // K quarters per panel
 constexpr int kWin = 2;     // chunks in flight per wave
 constexpr uint32_t kSlice = 32;  // activation rows per workgroup
 
@@ -38,42 +40,78 @@ __device__ inline rsrc_t make_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, (int)bytes, 0x00020000);
 }
 
-// One chunk's loads for a lane: two weight units, the block scale and the 32
-// activations of its (row, block) pair.
+// Per-wave constants of the loads.
+template <int P>
+struct Plan {
+  rsrc_t wq, ws, xr;
+  uint32_t K;
+  uint32_t p[P], R[P];           // panels (clamped to the last one) and their row counts
+  uint32_t w_voff[P], s_voff[P];  // this lane's unit / scale offsets in each panel
+  uint32_t x_voff;               // this lane's activation offset (coalesced pattern)
+};
+
+// One chunk's loads for a lane: two weight units and the block scale per
+// panel, and 8 x 16 bytes of activations in a coalesced pattern: piece i is
+// row 4i + lane/16, floats 4 * (lane % 16) .. +3 of the chunk (each load
+// instruction reads four whole 256-byte row segments).
+template <int P>
 struct Chunk {
-  u32x4 w[2];
-  uint32_t s;
+  u32x4 w[P][2];
+  uint32_t s[P];
   f32x4 x[8];
 };
 
-__device__ inline void load_chunk(Chunk &b, rsrc_t wq, rsrc_t ws, rsrc_t xr, uint32_t K,
-                                  uint32_t c, uint32_t p, uint32_t R, uint32_t w_voff,
-                                  uint32_t s_voff, uint32_t x_voff) {
-  const uint32_t so = (uint32_t)panel_chunk_qs(K, p, R, c);
-  b.w[0] = __builtin_amdgcn_raw_buffer_load_b128(wq, w_voff, so, 0);
-  b.w[1] = __builtin_amdgcn_raw_buffer_load_b128(wq, w_voff + 2 * R * 16, so, 0);
-  b.s = __builtin_amdgcn_raw_buffer_load_b16(ws, s_voff, (uint32_t)panel_chunk_sc(K, p, R, c) * 2, 0);
+template <int P>
+__device__ inline void load_chunk(Chunk<P> &b, const Plan<P> &pl, uint32_t c) {
+#pragma unroll
+  for (int t = 0; t < P; ++t) {
+    const uint32_t so = (uint32_t)panel_chunk_qs(pl.K, pl.p[t], pl.R[t], c);
+    b.w[t][0] = __builtin_amdgcn_raw_buffer_load_b128(pl.wq, pl.w_voff[t], so, 0);
+    b.w[t][1] = __builtin_amdgcn_raw_buffer_load_b128(pl.wq, pl.w_voff[t] + 2 * pl.R[t] * 16, so, 0);
+    b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(
+        pl.ws, pl.s_voff[t], (uint32_t)panel_chunk_sc(pl.K, pl.p[t], pl.R[t], c) * 2, 0);
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i)
-    b.x[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, x_voff + i * 16, c * kChunkK * 4, 0));
+    b.x[i] = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(pl.xr, pl.x_voff + i * 16 * pl.K, c * kChunkK * 4, 0));
 }
 
-// acc += W(chunk) . X(chunk)^T over the four k-steps; step s uses half (s & 1)
-// of weight unit s >> 1
-__device__ inline void accumulate(const Chunk &b, f32x16 &acc) {
-  const f16 sc = __builtin_bit_cast(f16, (uint16_t)b.s);
-  const f16x2 s2 = {sc, sc};
+// The wave's activation tile of one chunk in LDS: 32 rows x 64 f16, 128 bytes
+// per row, 16-byte pieces of row c XOR-swizzled by (c >> 1) & 7 so the
+// fragment reads (32 rows, one piece each) and the staging writes spread over
+// all banks.
+__device__ inline uint32_t x_piece(uint32_t row, uint32_t j) {
+  return row * 128 + ((j ^ ((row >> 1) & 7)) * 16);
+}
+
+// acc[t] += W_t(chunk) . X(chunk)^T over the four k-steps; step s uses half
+// (s & 1) of weight unit s >> 1 and activation piece 4h + s of row c.
+template <int P>
+__device__ inline void accumulate(const Chunk<P> &b, uint8_t *xt, uint32_t lane,
+                                  f32x16 (&acc)[P]) {
+  const uint32_t h = lane >> 5, c = lane & 31;
+  // stage: f32 -> f16 (round to nearest even, the kCvt32 staging), 8 bytes per piece
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t row = 4 * i + (lane >> 4), k4 = lane & 15;  // floats 4*k4 .. +3
+    const f16x4 v = {(f16)b.x[i].x, (f16)b.x[i].y, (f16)b.x[i].z, (f16)b.x[i].w};
+    *reinterpret_cast<f16x4 *>(xt + x_piece(row, k4 >> 1) + (k4 & 1) * 8) = v;
+  }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const u32x4 u = b.w[s >> 1];
-    const uint32_t b0 = (s & 1) ? u.z : u.x, b1 = (s & 1) ? u.w : u.y;
-    const f16x2 a0 = dequant_pair(b0, kSelLo, s2), a1 = dequant_pair(b0, kSelHi, s2);
-    const f16x2 a2 = dequant_pair(b1, kSelLo, s2), a3 = dequant_pair(b1, kSelHi, s2);
-    const f16x8 wf = {a0.x, a0.y, a1.x, a1.y, a2.x, a2.y, a3.x, a3.y};
-    const f32x4 lo = b.x[2 * s], hi = b.x[2 * s + 1];
-    const f16x8 xf = {(f16)lo.x, (f16)lo.y, (f16)lo.z, (f16)lo.w,
-                      (f16)hi.x, (f16)hi.y, (f16)hi.z, (f16)hi.w};
-    acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, xf, acc, 0, 0, 0);
+    const f16x8 xf = *reinterpret_cast<const f16x8 *>(xt + x_piece(c, 4 * h + s));
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+      const f16x2 s2 = {__builtin_bit_cast(f16, (uint16_t)b.s[t]),
+                        __builtin_bit_cast(f16, (uint16_t)b.s[t])};
+      const u32x4 u = b.w[t][s >> 1];
+      const uint32_t b0 = (s & 1) ? u.z : u.x, b1 = (s & 1) ? u.w : u.y;
+      const f16x2 a0 = dequant_pair(b0, kSelLo, s2), a1 = dequant_pair(b0, kSelHi, s2);
+      const f16x2 a2 = dequant_pair(b1, kSelLo, s2), a3 = dequant_pair(b1, kSelHi, s2);
+      const f16x8 wf = {a0.x, a0.y, a1.x, a1.y, a2.x, a2.y, a3.x, a3.y};
+      acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(wf, xf, acc[t], 0, 0, 0);
+    }
   }
 }
 
@@ -83,77 +121,121 @@ struct SkinnyArgs {
   const uint8_t *qs;
   const f16 *sc;
   uint32_t m, n, k;
-  uint32_t panels, slices;
+  uint32_t groups, slices;  // panel groups (P panels each) and 32-row activation slices
 };
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void q8_skinny_kernel(
+// LDS: the four waves' activation tiles during the K loop, then the partial
+// sums of the reduction
+template <int P, int KW>
+constexpr int skinny_lds() {
+  return (KW * 4096 > KW * P * 4 * 64 * 16) ? KW * 4096 : KW * P * 4 * 64 * 16;
+}
+
+// P panels per workgroup, KW waves splitting K
+template <int P, int KW, int WPE>
+__global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void q8_skinny_kernel(
     SkinnyArgs a) {
-  __shared__ __attribute__((aligned(16))) f32x4 red[kWaves][4][64];  // [wave][g][lane]
+  __shared__ __attribute__((aligned(16))) uint8_t smem[skinny_lds<P, KW>()];
 
   // Consecutive workgroups go to different XCDs (round-robin).  Map the
-  // slices of one panel to one XCD so they share its weights in that L2:
-  // workgroup b runs on XCD b % 8 and takes panel 8 * ((b / 8) / S) + b % 8,
+  // slices of one panel group to one XCD so they share its weights in that
+  // L2: workgroup b runs on XCD b % 8 and takes group 8 * ((b / 8) / S) + b % 8,
   // slice (b / 8) % S.
   const uint32_t b = blockIdx.x, S = a.slices;
-  const uint32_t p = 8 * ((b / 8) / S) + b % 8, slice = (b / 8) % S;
-  if (p >= a.panels) return;
+  const uint32_t grp = 8 * ((b / 8) / S) + b % 8, slice = (b / 8) % S;
+  if (grp >= a.groups) return;
 
   const uint32_t K = a.k, C = K / kChunkK;
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
-  const uint32_t R = panel_rows(a.n, p);
-  const uint32_t c0 = (wave * C) / kWaves, c1 = ((wave + 1) * C) / kWaves;
+  const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
+  const uint32_t c0 = (wave * C) / KW, c1 = ((wave + 1) * C) / KW;
 
-  // Lanes past a partial panel's last row read row R-1 (in bounds; their sums
-  // are never stored).  The activation resource covers the slice's rows that
-  // exist, so rows past M read zeros.
-  const uint32_t rr = r < R ? r : R - 1;
-  const uint32_t w_voff = (h * R + rr) * 16, s_voff = (h * R + rr) * 2;
+  // Panels past N are clamped to the last one and lanes past a partial
+  // panel's last row read row R-1 (in bounds; their sums are never stored).
+  // The activation resource covers the slice's rows that exist, so rows past
+  // M read zeros.
+  Plan<P> pl;
+  pl.K = K;
+  pl.wq = make_rsrc(a.qs, a.n * K);
+  pl.ws = make_rsrc(a.sc, a.n * (K / 32) * 2);
+#pragma unroll
+  for (int t = 0; t < P; ++t) {
+    const uint32_t pp = grp * P + t < np ? grp * P + t : np - 1;
+    pl.p[t] = pp;
+    pl.R[t] = panel_rows(a.n, pp);
+    const uint32_t rr = r < pl.R[t] ? r : pl.R[t] - 1;
+    pl.w_voff[t] = (h * pl.R[t] + rr) * 16;
+    pl.s_voff[t] = (h * pl.R[t] + rr) * 2;
+  }
   const uint32_t m0 = slice * kSlice;
   const uint32_t rows = a.m - m0 < kSlice ? a.m - m0 : kSlice;
-  const rsrc_t wq = make_rsrc(a.qs, a.n * K), ws = make_rsrc(a.sc, a.n * (K / 32) * 2);
-  const rsrc_t xr = make_rsrc(a.x + (size_t)m0 * K, rows * K * 4);
-  const uint32_t x_voff = r * K * 4 + h * 32 * 4;
+  pl.xr = make_rsrc(a.x + (size_t)m0 * K, rows * K * 4);
+  pl.x_voff = (lane >> 4) * K * 4 + (lane & 15) * 16;
 
-  Chunk win[kWin];
+  uint8_t *xt = smem + wave * 4096;
+  Chunk<P> win[kWin];
 #pragma unroll
   for (int i = 0; i < kWin; ++i)
-    if (c0 + i < c1) load_chunk(win[i], wq, ws, xr, K, c0 + i, p, R, w_voff, s_voff, x_voff);
-  f32x16 acc = {};
+    if (c0 + i < c1) load_chunk<P>(win[i], pl, c0 + i);
+  f32x16 acc[P];
+#pragma unroll
+  for (int t = 0; t < P; ++t) acc[t] = (f32x16){};
 #pragma unroll 1
   for (uint32_t c = c0; c < c1; c += kWin) {
 #pragma unroll
     for (int i = 0; i < kWin; ++i) {
       if (c + i < c1) {
-        accumulate(win[i], acc);
-        if (c + i + kWin < c1)
-          load_chunk(win[i], wq, ws, xr, K, c + i + kWin, p, R, w_voff, s_voff, x_voff);
+        accumulate<P>(win[i], xt, lane, acc);
+        if (c + i + kWin < c1) load_chunk<P>(win[i], pl, c + i + kWin);
       }
     }
   }
 
-  // Lane (h, c) holds D[n][m] for m = m0 + c and n = 32p + 8g + 4h + e
-  // (acc[4g + e]).  Wave w sums group g = w over the four K quarters.
+  // Lane (h, c) holds D[n][m] of panel t for m = m0 + c and
+  // n = 32 p_t + 8g + 4h + e (acc[t][4g + e]).  Wave w < 4 sums group g = w
+  // of every panel over the KW K ranges.
+  __syncthreads();  // every wave is done with its activation tile
+  f32x4 *red = reinterpret_cast<f32x4 *>(smem);  // [wave][t][g][lane]
 #pragma unroll
-  for (int g = 0; g < 4; ++g)
-    red[wave][g][lane] = (f32x4){acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+  for (int t = 0; t < P; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      red[((wave * P + t) * 4 + g) * 64 + lane] =
+          (f32x4){acc[t][4 * g], acc[t][4 * g + 1], acc[t][4 * g + 2], acc[t][4 * g + 3]};
   __syncthreads();
-  const f32x4 v = red[0][wave][lane] + red[1][wave][lane] + red[2][wave][lane] + red[3][wave][lane];
   const uint32_t m = m0 + r;
+  if (wave >= 4 || m >= a.m) return;
   const uint32_t nl = wave * 8 + h * 4;  // panel-local row of v.x
-  if (m >= a.m) return;
-  float *o = a.out + (size_t)m * a.n + p * kPanelRows + nl;
-  if (nl + 4 <= R) {
-    o[0] = v.x;
-    o[1] = v.y;
-    o[2] = v.z;
-    o[3] = v.w;
-  } else {
-    if (nl + 0 < R) o[0] = v.x;
-    if (nl + 1 < R) o[1] = v.y;
-    if (nl + 2 < R) o[2] = v.z;
+#pragma unroll
+  for (int t = 0; t < P; ++t) {
+    if (grp * P + t >= np) break;
+    f32x4 v = red[((0 * P + t) * 4 + wave) * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) v += red[((w * P + t) * 4 + wave) * 64 + lane];
+    const uint32_t R = pl.R[t];
+    float *o = a.out + (size_t)m * a.n + pl.p[t] * kPanelRows + nl;
+    if (nl + 4 <= R) {
+      o[0] = v.x;
+      o[1] = v.y;
+      o[2] = v.z;
+      o[3] = v.w;
+    } else {
+      if (nl + 0 < R) o[0] = v.x;
+      if (nl + 1 < R) o[1] = v.y;
+      if (nl + 2 < R) o[2] = v.z;
+    }
   }
+}
+
+template <int P, int KW, int WPE>
+int launch_skinny(SkinnyArgs a) {
+  const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
+  a.groups = (np + P - 1) / P;
+  const uint32_t grid = (a.groups + 7) / 8 * 8 * a.slices;
+  hipLaunchKernelGGL((q8_skinny_kernel<P, KW, WPE>), dim3(grid), dim3(KW * 64), 0, stream(), a);
+  return check_launch("madi_q8_pproj");
 }
 
 }  // namespace
@@ -178,9 +260,11 @@ extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const 
   a.m = m;
   a.n = n;
   a.k = k;
-  a.panels = (n + kPanelRows - 1) / kPanelRows;
   a.slices = (m + kSlice - 1) / kSlice;
-  const uint32_t grid = (a.panels + 7) / 8 * 8 * a.slices;
-  hipLaunchKernelGGL(q8_skinny_kernel, dim3(grid), dim3(256), 0, stream(), a);
-  return check_launch("madi_q8_pproj");
+  // wide matrices (the vocab logits): four panels per workgroup share each
+  // activation load; narrow ones keep one panel per workgroup and split K
+  // eight ways for parallelism
+  const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
+  if (np >= 1024) return launch_skinny<4, 4, 2>(a);
+  return launch_skinny<1, 8, 2>(a);
 }
