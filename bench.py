@@ -17,7 +17,12 @@ when profiles/traffic_q8_fc1_gemm_vocab_gemv.md holds them, the measured HBM
 bytes per launch, plus the restated reference CPU path timed on this host's
 cores (a reported baseline only).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
+Beside the headline, "configs" reports the other measured workloads: the
+encoder GEMM set of one 30 s window (32 layers, independent weights), a
+batched decode step at M = 8 and 16 (skinny Q8 projections, cold weights) with
+the per-chunk cross-attention K|V GEMM, and the 16-window long-audio fc1/fc2.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-configs]
        python bench.py --calibrate-copy   (a plain 256 MiB device copy, the
                                            reference kernel for FETCH_SIZE /
                                            WRITE_SIZE scaling)
@@ -99,6 +104,152 @@ def cpu_baseline(threads: int):
     return res
 
 
+# ---------------------------------------------------------------- other configurations
+# Encoder projection shapes per layer (large-v3-turbo, d_model 1280, MLP 5120)
+ENC_LAYERS, DEC_LAYERS = 32, 4
+ENC_SHAPES = [("qkv", 3840, 1280), ("out", 1280, 1280), ("fc1", 5120, 1280), ("fc2", 1280, 5120)]
+DEC_SHAPES = [("self_qkv", 3840, 1280), ("self_out", 1280, 1280), ("cross_q", 1280, 1280),
+              ("cross_out", 1280, 1280), ("ffn_up", 5120, 1280), ("ffn_down", 1280, 5120)]
+
+
+def _timed(torch, stream, fn, reps):
+    """Average seconds per call of fn() over `reps` back-to-back calls."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for i in range(reps):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / reps
+
+
+def _upload_layer(q8, seed, n, k):
+    from madi_amd import synth
+    qs, sc = synth.q8_weight(np.random.default_rng(seed), n, k)
+    return q8.upload_q8(qs, sc)
+
+
+def config_encoder_window(torch, stream, q8, reps=3):
+    """The encoder GEMM set of one 30 s window: 32 layers x (q|k|v stacked
+    1280->3840, out 1280->1280, fc1 1280->5120 + bias + GELU, fc2 5120->1280 +
+    bias) at M = 1500, independent seeded weights per layer (668 MB, so every
+    layer's weights stream from HBM)."""
+    from madi_amd import synth
+    m = 1500
+    a = torch.from_numpy(synth.activations(np.random.default_rng(100), m, 5120).view(np.int16)).cuda()
+    c = torch.empty((m, 5120), dtype=torch.int16, device="cuda")
+    bias = torch.from_numpy(np.random.default_rng(101).standard_normal(5120).astype(np.float32)).cuda()
+    layers = [[_upload_layer(q8, 1000 + 4 * l + j, n, k) for j, (_, n, k) in enumerate(ENC_SHAPES)]
+              for l in range(ENC_LAYERS)]
+    torch.cuda.synchronize()
+
+    def window(_):
+        for ws in layers:
+            q8.kGemmQ8(a, ws[0], c, m, 3840, 1280)
+            q8.kGemmQ8(a, ws[1], c, m, 1280, 1280)
+            q8.kGemmQ8Bias(a, ws[2], c, bias, m, 5120, 1280, gelu=True)
+            q8.kGemmQ8Bias(a, ws[3], c, bias, m, 1280, 5120)
+
+    window(0)
+    t = _timed(torch, stream, window, reps)
+    flops = ENC_LAYERS * sum(2.0 * m * n * k for _, n, k in ENC_SHAPES)
+    per = {}
+    for j, (name, n, k) in enumerate(ENC_SHAPES):
+        def one(i, j=j, n=n, k=k):
+            ws = layers[i % ENC_LAYERS][j]
+            if j == 2:
+                q8.kGemmQ8Bias(a, ws, c, bias, m, n, k, gelu=True)
+            elif j == 3:
+                q8.kGemmQ8Bias(a, ws, c, bias, m, n, k)
+            else:
+                q8.kGemmQ8(a, ws, c, m, n, k)
+        tj = _timed(torch, stream, one, ENC_LAYERS)
+        per[name] = {"us": round(tj * 1e6, 2), "tflops": round(2.0 * m * n * k / tj / 1e12, 1)}
+    del layers
+    return {
+        "workload": "32 layers x (qkv 1280->3840, out 1280->1280, fc1 1280->5120 +bias+GELU, "
+                    "fc2 5120->1280 +bias) Q8 GEMMs at M=1500, independent weights per layer",
+        "ms_per_window": round(t * 1e3, 4), "tflop_per_window": round(flops / 1e12, 4),
+        "tflops": round(flops / t / 1e12, 1),
+        "frac_fp16_peak": round(flops / t / 1e12 / PEAK_FP16_TFLOPS, 4),
+        "per_gemm_cold": per,
+    }
+
+
+def config_batched_decode(torch, stream, q8, reps=20):
+    """One batched decode step at M = 8 and 16 token rows: 4 decoder layers x
+    (self q|k|v 1280->3840, self out, cross q, cross out 1280->1280, FFN
+    1280->5120->1280) + vocab 1280->51866 through the skinny Q8 projection, two
+    alternating weight sets (2 x 168 MB > the 256 MB Infinity Cache); plus the
+    per-chunk cross-attention K|V projection 1280->2560 at M = 1500 (GEMM)."""
+    from madi_amd import synth
+    sets = []
+    for s_ in range(2):
+        layers = [[_upload_layer(q8, 2000 + 100 * s_ + 8 * l + j, n, k)
+                   for j, (_, n, k) in enumerate(DEC_SHAPES)] for l in range(DEC_LAYERS)]
+        vocab = _upload_layer(q8, 2900 + s_, VOCAB, DIM)
+        sets.append((layers, vocab))
+    xin = torch.from_numpy(np.random.default_rng(102).standard_normal((16, 5120)).astype(np.float32)).cuda()
+    out = torch.empty((16, VOCAB), dtype=torch.float32, device="cuda")
+    step_bytes = (DEC_LAYERS * sum(n * k + n * (k // 32) * 2 for _, n, k in DEC_SHAPES)
+                  + VOCAB * DIM + VOCAB * (DIM // 32) * 2)
+    res = {"workload": "batched decode step: 4 layers x (self qkv 1280->3840, self out, cross q, "
+                       "cross out 1280->1280, ffn 1280->5120->1280) + vocab 1280->51866, skinny "
+                       "Q8 projection, weights cold (two alternating sets)",
+           "weight_bytes_per_step": step_bytes}
+    for m in (8, 16):
+        def step(i, m=m):
+            layers, vocab = sets[i % 2]
+            for ws in layers:
+                for j, (_, n, k) in enumerate(DEC_SHAPES):
+                    q8.pproj(xin, ws[j], out, m, n, k)
+            q8.pproj(xin, vocab, out, m, VOCAB, DIM)
+        step(0)
+        step(1)
+        t = _timed(torch, stream, step, reps)
+        byts = step_bytes + DEC_LAYERS * sum(m * k * 4 + m * n * 4 for _, n, k in DEC_SHAPES) \
+            + m * DIM * 4 + m * VOCAB * 4
+        res[f"m{m}"] = {"us_per_step": round(t * 1e6, 2), "gbs": round(byts / t / 1e9, 1),
+                        "frac_hbm_peak": round(byts / t / 1e9 / PEAK_HBM_GBS, 4)}
+        tv = _timed(torch, stream, lambda i, m=m: q8.pproj(xin, sets[i % 2][1], out, m, VOCAB, DIM),
+                    reps)
+        vb = VOCAB * DIM + VOCAB * (DIM // 32) * 2 + m * DIM * 4 + m * VOCAB * 4
+        res[f"m{m}"]["vocab_us"] = round(tv * 1e6, 2)
+        res[f"m{m}"]["vocab_frac_hbm_peak"] = round(vb / tv / 1e9 / PEAK_HBM_GBS, 4)
+    del sets
+    m = 1500
+    ctx = torch.from_numpy(synth.activations(np.random.default_rng(103), m, DIM).view(np.int16)).cuda()
+    kv = torch.empty((m, 2560), dtype=torch.int16, device="cuda")
+    wkv = [_upload_layer(q8, 2990 + l, 2560, DIM) for l in range(DEC_LAYERS)]
+    q8.kGemmQ8(ctx, wkv[0], kv, m, 2560, DIM)
+    t = _timed(torch, stream, lambda i: q8.kGemmQ8(ctx, wkv[i % DEC_LAYERS], kv, m, 2560, DIM), 20)
+    fl = 2.0 * m * 2560 * DIM
+    res["cross_kv_m1500"] = {"us": round(t * 1e6, 2), "tflops": round(fl / t / 1e12, 1),
+                             "frac_fp16_peak": round(fl / t / 1e12 / PEAK_FP16_TFLOPS, 4)}
+    return res
+
+
+def config_long_audio(torch, stream, q8, reps=5):
+    """16 stacked 30 s windows: fc1 M=24000 K=1280 N=5120 and fc2 M=24000
+    K=5120 N=1280 Q8 GEMMs."""
+    import torch as _t  # noqa: F401
+    m = 24000
+    g = torch.Generator(device="cuda").manual_seed(104)
+    a = torch.randn((m, 5120), generator=g, device="cuda", dtype=torch.float32).half().view(torch.int16)
+    c = torch.empty((m, 5120), dtype=torch.int16, device="cuda")
+    res = {"workload": "fc1 M=24000 K=1280 N=5120, fc2 M=24000 K=5120 N=1280 Q8 GEMMs "
+                       "(activations drawn on the device: torch Philox N(0,1) -> f16)"}
+    for name, n, k in (("fc1", 5120, 1280), ("fc2", 1280, 5120)):
+        w = _upload_layer(q8, 3000 + n, n, k)
+        q8.kGemmQ8(a, w, c, m, n, k)
+        t = _timed(torch, stream, lambda i: q8.kGemmQ8(a, w, c, m, n, k), reps)
+        fl = 2.0 * m * n * k
+        res[name] = {"us": round(t * 1e6, 1), "tflops": round(fl / t / 1e12, 1),
+                     "frac_fp16_peak": round(fl / t / 1e12 / PEAK_FP16_TFLOPS, 4)}
+    return res
+
+
 def measured_traffic():
     """HBM bytes per launch {kernel: bytes} from the committed PMC summary, if any."""
     out = {}
@@ -139,6 +290,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the encoder-window, batched-decode and long-audio measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (PMC calibration)")
     args = ap.parse_args()
@@ -242,6 +395,14 @@ def main():
             },
         },
     }
+    if not args.no_configs:
+        log("encoder window (32 layers x 4 GEMMs at M=1500)")
+        cfg = {"encoder_window": config_encoder_window(torch, stream, q8)}
+        log("batched decode (M=8, 16)")
+        cfg["batched_decode"] = config_batched_decode(torch, stream, q8)
+        log("long audio (M=24000)")
+        cfg["long_audio"] = config_long_audio(torch, stream, q8)
+        result["configs"] = cfg
     if not args.no_cpu:
         threads = min(16, os.cpu_count() or 1)
         log(f"cpu baseline on {threads} threads ({cpu_model()})")

@@ -15,6 +15,10 @@ int fail(int code, const char *fmt, ...);
 int check_launch(const char *what);
 bool initialized();
 hipStream_t stream();
+// The library's split-K workspace: `partial_bytes` of fp32 partial sums and
+// `counters` arrival counters that are zero whenever no kernel is using them.
+// Grows on demand (a grow waits for the device); freed by madi_cleanup.
+int workspace(size_t partial_bytes, size_t counters, float **partials, uint32_t **cnt);
 
 inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 

@@ -48,6 +48,12 @@
 // touching memory, so they add exact zeros.  Loads are issued in the same
 // pattern every chunk, which keeps every vmcnt wait a constant.
 //
+// Split K: when the tiles alone cannot fill the GPU and K is long (fc2,
+// 5120 -> 1280 at M = 1500, makes 60 tiles), up to four workgroups share a
+// tile, each over a contiguous K range.  Each publishes its fp32 partial tile
+// to the library's workspace and counts itself in with a system-scope atomic;
+// the last to arrive adds the other partials and runs the epilogue.
+//
 // Epilogue: bias / GELU in fp32 registers, one rounding to f16, then the tile
 // is transposed through LDS so every global store writes whole 512-byte row
 // segments (16 bytes per lane).
@@ -282,17 +288,24 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
                                                       f16 *__restrict__ Cout,
                                                       const float *__restrict__ bias, uint32_t M,
                                                       uint32_t N, uint32_t K, uint32_t tiles_m,
-                                                      uint32_t tiles_n, uint32_t group_m) {
+                                                      uint32_t tiles_n, uint32_t group_m,
+                                                      uint32_t splits, float *__restrict__ ws,
+                                                      uint32_t *__restrict__ cnt) {
   using G = Geometry<MT>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G::kLds];
+  __shared__ uint32_t arrived;
 
   // ---- tile order: consecutive workgroups go to different XCDs (round-robin),
   // so renumber to give each XCD a contiguous run, then walk that run in
   // groups of `group_m` M-tiles so an XCD's tiles share A rows and W panels
-  // in its own L2.
+  // in its own L2.  With split K, workgroup (split, tile) covers K chunks
+  // [split * C / splits, (split + 1) * C / splits) of tile `tile`.
   const uint32_t T = tiles_m * tiles_n;
   uint32_t bid = blockIdx.x;
-  if (T % 8 == 0) bid = (bid % 8) * (T / 8) + bid / 8;
+  if ((T * splits) % 8 == 0) bid = (bid % 8) * (T * splits / 8) + bid / 8;
+  const uint32_t split = bid / T;
+  bid %= T;
+  const uint32_t tile = bid;
   const uint32_t per_group = group_m * tiles_n;
   const uint32_t gi = bid / per_group, first_m = gi * group_m;
   const uint32_t gm = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
@@ -303,7 +316,8 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
   const uint32_t m0 = tm * 32 * MT, p0 = tn * kPanelsPerTile;
-  const uint32_t np = N / kPanelRows, nchunks = K / kChunkK;
+  const uint32_t np = N / kPanelRows, call = K / kChunkK;
+  const uint32_t cb = split * call / splits, nchunks = (split + 1) * call / splits - cb;
 
   // ---- load plan.  Panels past N and rows past M are clamped to the last
   // valid one: their bytes are read but their results are never stored.
@@ -317,8 +331,8 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   for (int t = 0; t < 2; ++t) {
     uint32_t pp = p0 + 2 * wave + t;
     pp = pp < np ? pp : np - 1;
-    p.w_soff[t] = pp * kPanelRows * K;
-    p.s_voff[t] = pp * K * 2 + lane * 2;  // panel pp's chunk c scales at pp*K + 64c elements
+    p.w_soff[t] = pp * kPanelRows * K + cb * 2048;
+    p.s_voff[t] = pp * K * 2 + cb * 128 + lane * 2;  // panel pp's chunk c scales at pp*K + 64c elements
   }
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
@@ -326,7 +340,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
     const uint32_t q = (lane & 7) ^ a_swz(row);
     uint32_t m = m0 + row;
     m = m < M ? m : M - 1;
-    p.a_voff[i] = m * K * 2 + q * 16;
+    p.a_voff[i] = m * K * 2 + cb * 128 + q * 16;
   }
 
   f32x16 acc[2][MT];
@@ -361,7 +375,9 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   for (int s = 0; s < 3; ++s) w[1][s] = dequant_frag(r0, 1, s);
   load_a_frags<MT>(smem, 0, h, r, af);
 
-  // ---- main loop: four chunks per trip (the weight register sets rotate)
+  // ---- main loop: four chunks per trip (the weight register sets rotate).
+  // The loop body stays one straight-line block: extra exits let the register
+  // allocator copy asm-loaded registers before their vmcnt wait.
   const uint32_t cpad = (nchunks + WD - 1) / WD * WD;
   for (uint32_t c = 0; c < cpad; c += 4) {
     chunk<MT>(smem, p, c + 0, wave, lane, h, r, acc, w, af, r0, r1, r0);
@@ -374,6 +390,56 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   // n = 32(2w + t) + 8g + 4h + e (acc[t][i][4g + e]).  Every wave must finish
   // reading the ring before it becomes the C tile.
   wait_then_barrier<0>();
+  if (splits > 1) {
+    // Split K: every workgroup of the tile publishes its partial sums (in
+    // register order, so each lane later reads back exactly what it wrote) and
+    // counts itself in; the last to arrive adds the others' partials to its
+    // own and finishes the tile.  The partials are written and read with
+    // device-scope (sc1) buffer accesses, which write through and read past
+    // the XCD's own L2, and the count is a system-scope atomic, so no L2-wide
+    // writeback or invalidate is needed.
+    constexpr uint32_t kPart = 4 * 2 * MT * 4 * 64 * 16;  // bytes per partial tile
+    constexpr int kSc1 = 16;                             // cache policy: sc1
+    const __amdgpu_buffer_rsrc_t wsr =
+        __builtin_amdgcn_make_buffer_rsrc(ws, 0, (int)(T * splits * kPart), 0x00020000);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < MT; ++i)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, (f32x4){acc[t][i][4 * g], acc[t][i][4 * g + 1],
+                                                acc[t][i][4 * g + 2], acc[t][i][4 * g + 3]}),
+              wsr, ((((wave * 2 + t) * MT + i) * 4 + g) * 64 + lane) * 16,
+              (tile * splits + split) * kPart, kSc1);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial has been written through
+    __syncthreads();
+    if (threadIdx.x == 0)
+      arrived = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+    if (arrived != splits - 1) return;
+    for (uint32_t s2 = 0; s2 < splits; ++s2) {
+      if (s2 == split) continue;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4 v = __builtin_bit_cast(
+                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                           wsr, ((((wave * 2 + t) * MT + i) * 4 + g) * 64 + lane) * 16,
+                           (tile * splits + s2) * kPart, kSc1));
+            acc[t][i][4 * g] += v.x;
+            acc[t][i][4 * g + 1] += v.y;
+            acc[t][i][4 * g + 2] += v.z;
+            acc[t][i][4 * g + 3] += v.w;
+          }
+    }
+    if (threadIdx.x == 0)  // ready for the next launch
+      __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
   uint8_t *Ct = smem;
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
@@ -427,8 +493,27 @@ int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const fl
   const uint32_t tiles_m = (M + 32 * MT - 1) / (32 * MT);
   const uint32_t tiles_n = (N + 255) / 256;
   const uint32_t group_m = tiles_m < 6 ? tiles_m : 6;
-  hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI>), dim3(tiles_m * tiles_n), dim3(kWaves * 64), 0,
-                     stream(), A, qs, sc, C, bias, M, N, K, tiles_m, tiles_n, group_m);
+  const uint32_t T = tiles_m * tiles_n, chunks = K / kChunkK;
+  // Too few tiles to fill the GPU and a long K (fc2 at M = 1500: 60 tiles, 80
+  // chunks): split K over up to four workgroups per tile, >= 16 chunks each.
+  // The partial sums travel through memory (about 1 us per MB of partials),
+  // which only pays off when each split keeps a long K range.
+  uint32_t splits = 1;
+  if (T < 160 && chunks >= 64) {
+    splits = 240 / T;
+    if (splits > 4) splits = 4;
+    if (splits > chunks / 16) splits = chunks / 16;
+    if (splits < 1) splits = 1;
+  }
+  float *ws = nullptr;
+  uint32_t *cnt = nullptr;
+  if (splits > 1) {
+    const size_t part = (size_t)T * splits * (4 * 2 * MT * 4 * 64 * 16);
+    const int rc = workspace(part, T, &ws, &cnt);
+    if (rc != MADI_OK) return rc;
+  }
+  hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI>), dim3(T * splits), dim3(kWaves * 64), 0, stream(),
+                     A, qs, sc, C, bias, M, N, K, tiles_m, tiles_n, group_m, splits, ws, cnt);
   return check_launch("madi_q8_gemm");
 }
 

@@ -16,7 +16,46 @@ thread_local char g_err[512] = "";
 bool g_init = false;
 int g_cu_count = 0;
 hipStream_t g_stream = nullptr;
+// Split-K workspace: kCounters zeroed arrival counters, then the partial sums.
+constexpr size_t kCounters = 16384;
+void *g_ws = nullptr;
+size_t g_ws_bytes = 0;
+
+void free_workspace() {
+  if (g_ws) {
+    (void)hipDeviceSynchronize();
+    (void)hipFree(g_ws);
+  }
+  g_ws = nullptr;
+  g_ws_bytes = 0;
+}
 }  // namespace
+
+int workspace(size_t partial_bytes, size_t counters, float **partials, uint32_t **cnt) {
+  if (counters > kCounters)
+    return fail(MADI_ERR_SHAPE, "split-K workspace: %zu tiles exceed %zu", counters, kCounters);
+  const size_t need = kCounters * 4 + partial_bytes;
+  if (need > g_ws_bytes) {
+    // kernels still running may hold the old buffer: free_workspace waits for them
+    free_workspace();
+    hipError_t e = hipMalloc(&g_ws, need);
+    if (e != hipSuccess) {
+      g_ws = nullptr;
+      return fail(MADI_ERR_ALLOC, "split-K workspace (%zu bytes): %s", need, hipGetErrorString(e));
+    }
+    // the counters start at zero; every use returns them to zero
+    e = hipMemset(g_ws, 0, kCounters * 4);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      free_workspace();
+      return fail(MADI_ERR_ALLOC, "split-K workspace: clearing the counters: %s", hipGetErrorString(e));
+    }
+    g_ws_bytes = need;
+  }
+  *cnt = static_cast<uint32_t *>(g_ws);
+  *partials = reinterpret_cast<float *>(static_cast<uint8_t *>(g_ws) + kCounters * 4);
+  return MADI_OK;
+}
 
 int fail(int code, const char *fmt, ...) {
   va_list ap;
@@ -63,6 +102,7 @@ extern "C" int madi_init(void) {
 extern "C" void madi_cleanup(void) {
   if (!g_init) return;
   (void)hipStreamSynchronize(g_stream);
+  free_workspace();
   g_stream = nullptr;
   g_init = false;
 }

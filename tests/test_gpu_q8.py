@@ -140,6 +140,24 @@ def test_gemm_parity_small(q, m, n, k):
     assert tight_ok(c, a, qs, sc)
 
 
+@pytest.mark.parametrize("m,n,k", [
+    (257, 1280, 5120),  # 15 tiles x 4 K splits of 20 chunks, M tail
+    (20, 512, 4096),    # 32-row tiles, 2 tiles x 4 splits of 16 chunks
+    (64, 768, 6144),    # 64-row tiles, 3 tiles x 4 splits of 24 chunks
+])
+def test_gemm_split_k(q, m, n, k):
+    """Long K over few tiles: the workgroups of a tile split K and the last
+    to finish adds the others' partial sums (run twice: the arrival counters
+    must return to zero)."""
+    say(f"gemm split-K m={m} n={n} k={k}")
+    a, qs, sc = synth.gemm_case(m + n + k, m, n, k)
+    ref = O.q8_gemm_rows(a, qs, sc, threads=8)
+    for _ in range(2):
+        c = _gemm(q, a, qs, sc)
+        assert normwise(c, ref) <= TOL, normwise(c, ref)
+        assert tight_ok(c, a, qs, sc)
+
+
 def test_gemm_one_hot_is_dequant(q):
     """A = identity rows: each output row is one dequantised weight column,
     bit-exact (one exact product, fp32 sum of zeros, exact f16 store)."""
