@@ -36,6 +36,13 @@ int workspace(size_t partial_bytes, size_t counters, float **partials, uint32_t 
     return fail(MADI_ERR_SHAPE, "split-K workspace: %zu tiles exceed %zu", counters, kCounters);
   const size_t need = kCounters * 4 + partial_bytes;
   if (need > g_ws_bytes) {
+    // growing allocates and synchronises, which a stream under graph capture
+    // cannot do: the caller makes one such call before capturing
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g_stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(MADI_ERR_ARG,
+                  "split-K workspace must grow to %zu bytes, which cannot happen during graph "
+                  "capture; run this GEMM shape once before capturing", need);
     // kernels still running may hold the old buffer: free_workspace waits for them
     free_workspace();
     hipError_t e = hipMalloc(&g_ws, need);

@@ -347,3 +347,49 @@ def test_pproj_one_hot_is_dequant(q):
     c = _pproj(q, x, qs, sc)
     ref = O.dequant_q8_f16(qs, sc)[ks].astype(np.float32)  # [len(ks)][N]
     assert np.array_equal(c, ref)
+
+
+# ------------------------------------------------------------------ HIP graph replay
+def test_graph_replay_decode_sequence(q):
+    """A decode-style launch sequence (batched projection, GEMV, GEMM) captured
+    into a HIP graph: every replay, with eager work and synchronisations in
+    between, must match the eager results exactly (same kernels, same inputs)."""
+    say("graph replay")
+    rng = np.random.default_rng(31)
+    n1, k1 = 3840, 1280
+    qs1, sc1 = synth.q8_weight(rng, n1, k1)
+    w1 = q.upload_q8(qs1, sc1)
+    qs2, sc2 = synth.q8_weight(rng, 1280, 1280)
+    w2 = q.upload_q8(qs2, sc2)
+    x = dev(rng.standard_normal((8, k1)).astype(np.float32))
+    xv = dev(rng.standard_normal(k1).astype(np.float32))
+    a = dev_f16(synth.activations(rng, 300, 1280))
+    o1 = torch.empty((8, n1), dtype=torch.float32, device="cuda")
+    o2 = torch.empty(1280, dtype=torch.float32, device="cuda")
+    c = torch.empty((300, 1280), dtype=torch.int16, device="cuda")
+
+    def seq():
+        q.pproj(x, w1, o1, 8, n1, k1)
+        q.kGemvQ8(o2, xv, w2, 1280, 1280)
+        q.kGemmQ8(a, w2, c, 300, 1280, 1280)
+
+    seq()
+    q.sync()
+    want = (o1.clone(), o2.clone(), c.clone())
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            q.init(side)
+            seq()
+    q.init()  # back to the current stream for eager calls
+    for rep in range(4):
+        for t in (o1, o2):
+            t.fill_(float("nan"))
+        c.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o1, want[0]) and torch.equal(o2, want[1]) and torch.equal(c, want[2]), rep
+        seq()  # eager work between replays
+        q.sync()
