@@ -113,6 +113,17 @@ int madi_q8_unpack_host(void *dst_qs, void *dst_scales, const void *tiled_qs,
 int madi_q8_repack(void *dst_qs, void *dst_scales, const void *qs, const void *scales,
                    uint32_t n, uint32_t k);
 
+/* F16 [N][K] (natural, device) -> panel-layout Q8 (device), the loader's
+ * quantisation done on the GPU: per 32-block scale = max|w| / 127 (1.0 for an
+ * all-zero block) stored as f16, q = clamp(round_half_away(w * (1 / scale)), +-127),
+ * bit-identical to quantInto (transcribe.zig:309-326) followed by the repack.
+ * w must be 16-byte aligned. */
+int madi_q8_quantize(void *dst_qs, void *dst_scales, const void *w_f16, uint32_t n, uint32_t k);
+/* The WHASH weight identity: fnvQ8 (transcribe.zig:131-140), FNV-1a 64 over a
+ * NATURAL-layout weight's qs bytes (nq of them) then its nsc fp16 scales'
+ * bytes, continuing from `seed` (0xcbf29ce484222325 to start).  Host memory. */
+uint64_t madi_q8_fnv(uint64_t seed, const void *qs, size_t nq, const void *scales, size_t nsc);
+
 /* ---- ops (device pointers, panel-layout weights) ---------------------------- */
 /* Q8 -> F16 [K][N] transposed dequant, bit-exact fp16_rne(q * s).  Replaces
  * kDeq (engine/metal/encoder.zig:154-159) and deqW16 (transcribe.zig:4387-4393),

@@ -42,6 +42,8 @@ SIGNATURES = {
     "madi_q8_repack_host": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_unpack_host": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_repack": (_I, [_P, _P, _P, _P, _U32, _U32]),
+    "madi_q8_quantize": (_I, [_P, _P, _P, _U32, _U32]),
+    "madi_q8_fnv": (ctypes.c_uint64, [ctypes.c_uint64, _P, _SZ, _P, _SZ]),
     "madi_q8_dequant_f16": (_I, [_P, _P, _P, _U32, _U32]),
     "madi_q8_gemm": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _I]),
     "madi_q8_gemv": (_I, [_P, _P, _P, _P, _U32, _U32]),

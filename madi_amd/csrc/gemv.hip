@@ -13,14 +13,17 @@
 // panels) is resident from the start.
 //
 // The activation vector is loaded before the weights, staged once per
-// workgroup in LDS with its 32-wide block sums and read back as broadcast
-// 128-bit LDS loads.  v_perm_b32 turns two stored bytes u = q + 128 into the
-// exact fp16 pair 1024 + u (one VALU op per two weights); fp16 activations
-// accumulate x * (1024 + u) with v_dot2_f32_f16, fp32 activations with FMA,
-// and each block subtracts 1152 * sum(x) to leave sum(x * q).  Per
-// quantisation block the lane multiplies its partial by the block's scale, the
-// same (partial * scale) structure as the reference's kernels; the two
-// K-halves meet by a cross-lane shuffle and the four waves through LDS.
+// workgroup in LDS and read back as broadcast 128-bit LDS loads.  v_perm_b32
+// turns two stored bytes u = q + 128 into the fp16 pair 1024 + u and one
+// packed subtract of 1152 leaves the exact fp16 pair (q0, q1); fp16
+// activations accumulate x * q with v_dot2_f32_f16 (exact products, fp32
+// sums), fp32 activations with FMA.  Per quantisation block the lane
+// multiplies its partial by the block's scale, the (partial * scale)
+// structure of the reference's kernels; the two K-halves meet by a cross-lane
+// shuffle and the four waves through LDS.  (Accumulating x * (1024 + u) and
+// subtracting 1152 * sum(x) per block saves the subtract but cancels two
+// large sums: an all-zero block, whose scale is 1.0, then leaks ~1e-2 of
+// rounding noise into its row.)
 #include "common.h"
 
 using namespace madi;
@@ -51,10 +54,10 @@ struct GemvArgs {
   const uint32_t *pos;
 };
 
-// LDS bytes: x (K elements of XT), its K/32 block sums (fp32), the wave partials
+// LDS bytes: x (K elements of XT), the wave partials
 template <typename XT>
 constexpr size_t lds_bytes(uint32_t k) {
-  return (size_t)k * sizeof(XT) + (size_t)(k / 32) * 4 + kWaves * 32 * 4;
+  return (size_t)k * sizeof(XT) + kWaves * 32 * 4;
 }
 
 // One chunk's loads for a lane: its two 16-byte units and its block's scale.
@@ -79,10 +82,15 @@ __device__ inline void load_chunk(ChunkW &b, rsrc_t wq, rsrc_t ws, uint32_t K, u
   b.s = __builtin_amdgcn_raw_buffer_load_b16(ws, s_voff, (uint32_t)panel_chunk_sc(K, p, R, c) * 2, 0);
 }
 
-// sum_i x[i] * (1024 + u_i) over one 16-byte unit of biased bytes u = q + 128,
-// fp16 activations: v_perm_b32 turns two bytes into the exact fp16 pair
-// (1024 + u0, 1024 + u1) and v_dot2_f32_f16 accumulates both products in fp32
-// (each product is exact).  The caller removes 1152 * sum(x).
+// The exact fp16 pair (q0, q1) of two biased bytes of `w` selected by `sel`:
+// v_perm_b32 builds (1024 + u0, 1024 + u1), a packed subtract removes 1152.
+__device__ inline f16x2 q_pair(uint32_t w, uint32_t sel) {
+  const f16x2 bias = {(f16)-1152.0f, (f16)-1152.0f};
+  return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, sel)) + bias;
+}
+
+// sum_i x[i] * q[i] over one 16-byte unit, fp16 activations: v_dot2_f32_f16
+// multiplies two exact fp16 pairs (exact products) and adds them in fp32.
 __device__ inline float unit_dot(const u32x4 &w, const f16 *x16, float part) {
   const f16x8 xa = *reinterpret_cast<const f16x8 *>(x16);
   const f16x8 xb = *reinterpret_cast<const f16x8 *>(x16 + 8);
@@ -91,40 +99,34 @@ __device__ inline float unit_dot(const u32x4 &w, const f16 *x16, float part) {
   for (int d = 0; d < 4; ++d) {
     const f16x8 &xv = d < 2 ? xa : xb;
     const int e = (d & 1) * 4;
-    const f16x2 u01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, wd[d], kSelLo));
-    const f16x2 u23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, wd[d], kSelHi));
-    part = __builtin_amdgcn_fdot2(u01, (f16x2){xv[e], xv[e + 1]}, part, false);
-    part = __builtin_amdgcn_fdot2(u23, (f16x2){xv[e + 2], xv[e + 3]}, part, false);
+    part = __builtin_amdgcn_fdot2(q_pair(wd[d], kSelLo), (f16x2){xv[e], xv[e + 1]}, part, false);
+    part = __builtin_amdgcn_fdot2(q_pair(wd[d], kSelHi), (f16x2){xv[e + 2], xv[e + 3]}, part, false);
   }
   return part;
 }
 
-// The same sum for fp32 activations: v_fma_mix_f32 multiplies the fp32 x by
-// the fp16 value 1024 + u straight out of the perm (one rounding per step).
+// The same sum for fp32 activations: FMA of the fp32 x with the exact q.
 __device__ inline float unit_dot(const u32x4 &w, const float *x32, float part) {
   const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
     const f32x4 xv = *reinterpret_cast<const f32x4 *>(x32 + 4 * d);
-    const f16x2 u01 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, wd[d], kSelLo));
-    const f16x2 u23 = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, wd[d], kSelHi));
-    part = __builtin_fmaf(xv.x, (float)u01.x, part);
-    part = __builtin_fmaf(xv.y, (float)u01.y, part);
-    part = __builtin_fmaf(xv.z, (float)u23.x, part);
-    part = __builtin_fmaf(xv.w, (float)u23.y, part);
+    const f16x2 q01 = q_pair(wd[d], kSelLo), q23 = q_pair(wd[d], kSelHi);
+    part = __builtin_fmaf(xv.x, (float)q01.x, part);
+    part = __builtin_fmaf(xv.y, (float)q01.y, part);
+    part = __builtin_fmaf(xv.z, (float)q23.x, part);
+    part = __builtin_fmaf(xv.w, (float)q23.y, part);
   }
   return part;
 }
 
-// acc += scale * (sum_k x[k] q[k]) over the lane's quantisation block of chunk
-// c; q = (1024 + u) - 1152, so the block subtracts 1152 * (sum of its 32 x).
+// acc += scale * (sum_k x[k] q[k]) over the lane's quantisation block of chunk c
 template <typename XT>
-__device__ inline void accumulate(const ChunkW &b, uint32_t c, const XT *xs, const float *xsum,
-                                  uint32_t h, float &acc) {
+__device__ inline void accumulate(const ChunkW &b, uint32_t c, const XT *xs, uint32_t h,
+                                  float &acc) {
   const uint32_t k0 = c * kChunkK + h * 32;  // the lane's 32-wide block
   float part = unit_dot(b.w[0], xs + k0, 0.0f);
   part = unit_dot(b.w[1], xs + k0 + 16, part);
-  part = __builtin_fmaf(-1152.0f, xsum[k0 >> 5], part);
   acc = __builtin_fmaf(part, (float)__builtin_bit_cast(f16, (uint16_t)b.s), acc);
 }
 
@@ -132,10 +134,8 @@ template <typename XT, int MODE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q8_gemv_kernel(
     GemvArgs a) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  constexpr bool kF16 = sizeof(XT) == 2;
   const uint32_t K = a.k, C = K / kChunkK;
   XT *xs = reinterpret_cast<XT *>(smem);                        // [K]
-  float *xsum = reinterpret_cast<float *>(smem + K * sizeof(XT));  // [K/32]
   float *red = reinterpret_cast<float *>(smem + lds_bytes<XT>(K) - kWaves * 32 * 4);  // [4][32]
 
   const uint32_t lane = threadIdx.x & 63;
@@ -165,25 +165,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   for (int k = 0; k < kWin; ++k)
     if (c0 + k < c1) load_chunk(win[k], wq, ws, K, c0 + k, p, R, w_voff, s_voff);
 
-  // stage x and its 32-wide block sums (in fp32; the pieces of one block sit in
-  // 32 * sizeof(XT) / 16 adjacent lanes)
-  constexpr uint32_t kPer = 32 * sizeof(XT) / 16;  // 16-byte pieces per block
+  // stage x
   for (uint32_t i = threadIdx.x; i < pieces; i += 256) {
     const u32x4 v =
         i == i0 ? xv0 : (i == i1 ? xv1 : __builtin_amdgcn_raw_buffer_load_b128(xr, i * 16, 0, 0));
     reinterpret_cast<u32x4 *>(xs)[i] = v;
-    float sp;
-    if constexpr (kF16) {
-      const f16x8 f = __builtin_bit_cast(f16x8, v);
-      sp = (((float)f[0] + (float)f[1]) + ((float)f[2] + (float)f[3])) +
-           (((float)f[4] + (float)f[5]) + ((float)f[6] + (float)f[7]));
-    } else {
-      const f32x4 f = __builtin_bit_cast(f32x4, v);
-      sp = (f.x + f.y) + (f.z + f.w);
-    }
-#pragma unroll
-    for (uint32_t off = 1; off < kPer; off <<= 1) sp += __shfl_xor(sp, off, kPer);
-    if ((i & (kPer - 1)) == 0) xsum[i / kPer] = sp;
   }
   __syncthreads();
 
@@ -195,7 +181,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
 #pragma unroll
     for (int k = 0; k < kWin; ++k) {
       if (c + k < c1) {
-        accumulate<XT>(win[k], c + k, xs, xsum, h, acc);
+        accumulate<XT>(win[k], c + k, xs, h, acc);
         if (c + k + kWin < c1) load_chunk(win[k], wq, ws, K, c + k + kWin, p, R, w_voff, s_voff);
       }
     }

@@ -1,5 +1,6 @@
-// layout.hip -- load-time repack into the CDNA4 panel layout, the transposed
-// F16 dequant, and Q8 embedding-row gathers, all on the panel layout.
+// layout.hip -- load-time work on the CDNA4 panel layout: repack of natural Q8
+// rows, F16 -> Q8 quantisation straight into panels, the weight identity hash,
+// the transposed F16 dequant, and Q8 embedding-row gathers.
 #include <string.h>
 
 #include "common.h"
@@ -137,6 +138,83 @@ extern "C" int madi_q8_repack(void *dst_qs, void *dst_scales, const void *qs, co
                      stream(), static_cast<uint16_t *>(dst_scales),
                      static_cast<const uint16_t *>(scales), n, k, ns);
   return check_launch("madi_q8_repack(scales)");
+}
+
+// ------------------------------------------------------------------ quantise F16 -> panel Q8
+// quantInto (engine/metal/transcribe.zig:309-326) and quantize_q8.py:27-40 on
+// the device, writing straight into the panel layout.  One thread per
+// (row, 32-block): scale = max|w| / 127 in f32 (1.0 for an all-zero block),
+// stored as f16; q = clamp(round_half_away(w * (1 / scale)), -127, 127), all
+// in correctly rounded f32 as the Zig loop does.
+__global__ __launch_bounds__(256) void q8_quantize_kernel(uint8_t *__restrict__ dst_q,
+                                                          uint16_t *__restrict__ dst_s,
+                                                          const uint16_t *__restrict__ src,
+                                                          uint32_t n, uint32_t k, size_t blocks) {
+  const size_t u = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (u >= blocks) return;
+  const uint32_t nb = k / 32;
+  const uint32_t row = (uint32_t)(u / nb), b = (uint32_t)(u % nb);
+  const u32x4 *s4 = reinterpret_cast<const u32x4 *>(src + (size_t)row * k + (size_t)b * 32);
+  float w[32];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f16x8 v = __builtin_bit_cast(f16x8, s4[i]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[8 * i + e] = (float)v[e];
+  }
+  float mx = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float a = __builtin_fabsf(w[i]);
+    mx = a > mx ? a : mx;
+  }
+  const float scale = mx > 0.0f ? __fdiv_rn(mx, 127.0f) : 1.0f;
+  const float inv = __frcp_rn(scale);
+  uint32_t word[8];
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float q = roundf(__fmul_rn(w[4 * d + e], inv));
+      q = q < -127.0f ? -127.0f : (q > 127.0f ? 127.0f : q);
+      packed |= (uint32_t)((int)q + 128) << (8 * e);  // stored biased: q + 128
+    }
+    word[d] = packed;
+  }
+  const uint32_t p = row / kPanelRows, r = row % kPanelRows, R = panel_rows(n, p);
+  const uint32_t c = b / 2, h = b % 2;
+  uint8_t *chunk = dst_q + panel_chunk_qs(k, p, R, c);
+  *reinterpret_cast<u32x4 *>(chunk + ((0 + h) * R + r) * 16) = (u32x4){word[0], word[1], word[2], word[3]};
+  *reinterpret_cast<u32x4 *>(chunk + ((2 + h) * R + r) * 16) = (u32x4){word[4], word[5], word[6], word[7]};
+  dst_s[panel_chunk_sc(k, p, R, c) + h * R + r] = __builtin_bit_cast(uint16_t, (f16)scale);
+}
+
+extern "C" int madi_q8_quantize(void *dst_qs, void *dst_scales, const void *w_f16, uint32_t n,
+                                uint32_t k) {
+  if (!dst_qs || !dst_scales || !w_f16) return fail(MADI_ERR_NULL, "madi_q8_quantize: null pointer");
+  if (int rc = check_q8_shape("madi_q8_quantize", n, k)) return rc;
+  if (!aligned(dst_qs, 16) || !aligned(w_f16, 16) || !aligned(dst_scales, 2))
+    return fail(MADI_ERR_ALIGN, "madi_q8_quantize: qs and w need 16-byte alignment");
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_quantize: madi_init has not succeeded");
+  const size_t blocks = (size_t)n * (k / 32);
+  hipLaunchKernelGGL(q8_quantize_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
+                     stream(), static_cast<uint8_t *>(dst_qs), static_cast<uint16_t *>(dst_scales),
+                     static_cast<const uint16_t *>(w_f16), n, k, blocks);
+  return check_launch("madi_q8_quantize");
+}
+
+// ------------------------------------------------------------------ weight identity (host)
+// fnvQ8 (engine/metal/transcribe.zig:131-140): FNV-1a 64 over the natural-layout
+// qs bytes, then the scales' little-endian bytes, continuing from `seed`.
+extern "C" uint64_t madi_q8_fnv(uint64_t seed, const void *qs, size_t nq, const void *scales,
+                                size_t nsc) {
+  uint64_t x = seed;
+  const uint8_t *b = static_cast<const uint8_t *>(qs);
+  for (size_t i = 0; i < nq; ++i) x = (x ^ b[i]) * 0x100000001b3ull;
+  b = static_cast<const uint8_t *>(scales);
+  for (size_t i = 0; i < nsc * 2; ++i) x = (x ^ b[i]) * 0x100000001b3ull;
+  return x;
 }
 
 // ------------------------------------------------------------------ dequant -> F16 [K][N]

@@ -105,6 +105,27 @@ def upload_q8_device_repack(qs: np.ndarray, scales: np.ndarray, device="cuda") -
     return Q8(dq.data_ptr(), ds.data_ptr(), (dq, ds, nq, ns))
 
 
+def quantize(w16, n: int, k: int, device="cuda") -> Q8:
+    """Load-time quantisation on the GPU (quantInto, transcribe.zig:309-326, then
+    the repack): F16 [n][k] device tensor -> panel-layout Q8 on the device."""
+    import torch
+    dq = torch.empty(n * k, dtype=torch.uint8, device=device)
+    ds = torch.empty(n * (k // 32), dtype=torch.int16, device=device)
+    call("madi_q8_quantize", dq.data_ptr(), ds.data_ptr(), ptr(w16), n, k)
+    return Q8(dq.data_ptr(), ds.data_ptr(), (dq, ds))
+
+
+FNV_SEED = 0xcbf29ce484222325
+
+
+def fnv(seed: int, qs: np.ndarray, scales: np.ndarray) -> int:
+    """fnvQ8 (transcribe.zig:131-140) over a natural-layout Q8 weight in host
+    memory: FNV-1a 64 over the qs bytes, then the scales' bytes."""
+    qs = np.ascontiguousarray(qs)
+    scales = np.ascontiguousarray(scales, dtype=np.float16)
+    return int(lib().madi_q8_fnv(seed, qs.ctypes.data, qs.size, scales.ctypes.data, scales.size))
+
+
 # ---- encoder.zig -----------------------------------------------------------
 def kDeq(wdq, w: Q8, n: int, k: int) -> None:
     """encoder.zig:154-159: Q8 [N][K] -> F16 [K][N] (dequant_q8_f16)."""
@@ -183,7 +204,7 @@ def gemv_f16x(out, x16, w: Q8, n: int, k: int, bias=None, epilogue: int = EPI_NO
 
 __all__ = [
     "D", "MLP", "VOCAB", "ENC_SEQ", "Q8", "init", "sync", "repack_host", "unpack_host",
-    "upload_q8", "upload_q8_device_repack", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias",
+    "upload_q8", "upload_q8_device_repack", "quantize", "fnv", "FNV_SEED", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias",
     "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "pproj", "kQkv", "kLogitGemv", "embLookup",
     "embLookupIndirect", "gemv_f16x", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU",
     "EPI_BIAS_RES",

@@ -219,6 +219,30 @@ def test_gemv_parity(q, n, k):
     assert normwise(out2.cpu().numpy(), ref) <= 1e-5
 
 
+@pytest.mark.parametrize("x_f16", [False, True])
+def test_gemv_zero_blocks_are_exact(q, x_f16):
+    """All-zero quantisation blocks (scale 1.0) contribute exactly nothing:
+    a row of zero blocks gives exactly 0, and zero blocks mixed into a row
+    leave its sum at the oracle's to f32 rounding."""
+    n, k = 96, 1280
+    x16, qs, sc = synth.gemv_case(71, n, k)
+    qs[5, :] = 0
+    sc[5, :] = 1.0
+    qs[7, 64:256] = 0
+    sc[7, 2:8] = 1.0
+    w = q.upload_q8(qs, sc)
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    if x_f16:
+        q.gemv_f16x(out, dev_f16(x16), w, n, k)
+    else:
+        q.kGemvQ8(out, dev(x16.astype(np.float32)), w, n, k)
+    q.sync()
+    got = out.cpu().numpy()
+    assert got[5] == 0.0
+    ref = O.q8_gemv(x16.astype(np.float32), qs, sc, threads=4)
+    assert normwise(got, ref) <= 1e-5
+
+
 def test_logit_gemv_vocab(q):
     n, k = 51866, 1280
     x16, qs, sc = synth.gemv_case(0, n, k)
@@ -393,3 +417,58 @@ def test_graph_replay_decode_sequence(q):
         assert torch.equal(o1, want[0]) and torch.equal(o2, want[1]) and torch.equal(c, want[2]), rep
         seq()  # eager work between replays
         q.sync()
+
+
+# ------------------------------------------------------------------ load path: quantise, Q8 files
+def _knife_edge_weights(rng, n, k):
+    """Random f16 rows plus planted blocks: all zero (scale 1.0), exact half
+    steps (w / scale = q + 0.5 exactly: round half away from zero), a block
+    whose max maps to 127, and subnormal-range values (f16 subnormal scales)."""
+    w = (rng.standard_normal((n, k)) * 0.05).astype(np.float16)
+    w[0, 0:32] = 0
+    half = np.array([127, 0.5, 1.5, -2.5, 3.5, -126.5, 64.5, -0.5] * 4, np.float32) * 2.0**-7
+    w[1, 32:64] = half.astype(np.float16)
+    w[2, 0:32] = np.linspace(-1, 1, 32).astype(np.float16)
+    w[3, 64:96] = (rng.standard_normal(32) * 1e-6).astype(np.float16)
+    return w
+
+
+@pytest.mark.parametrize("n,k", [(100, 256), (51866, 1280)])
+def test_quantize_bit_exact(q, n, k):
+    say(f"quantize n={n} k={k}")
+    rng = np.random.default_rng(n)
+    w = _knife_edge_weights(rng, n, k)
+    got = q.quantize(dev_f16(w), n, k)
+    q.sync()
+    tq = got._keep[0].cpu().numpy()
+    ts = got._keep[1].cpu().numpy().view(np.float16)
+    uq, us = q.unpack_host(tq, ts, n, k)
+    rq, rs = O.quantize_q8(w)
+    assert np.array_equal(uq, rq)
+    assert np.array_equal(us.view(np.uint16), rs.view(np.uint16))
+
+
+def test_q8_file_load_equals_f16_quantize(q, tmp_path):
+    """The WHASH identity on the device: a weight loaded from a Q8 file (the
+    oracle's quantisation written as K.qs / K.scales) and the same weight
+    quantised from an F16 file on the GPU are the same panel bytes, and a GEMV
+    through it matches the oracle."""
+    st = pytest.importorskip("safetensors.numpy")
+    from madi_amd import loader
+    n, k = 3840, 1280
+    rng = np.random.default_rng(41)
+    w = _knife_edge_weights(rng, n, k)
+    rq, rs = O.quantize_q8(w)
+    f16_path, q8_path = tmp_path / "f16.safetensors", tmp_path / "q8.safetensors"
+    st.save_file({"dec.qkv": w}, str(f16_path))
+    st.save_file({"dec.qkv.qs": rq, "dec.qkv.scales": rs}, str(q8_path))
+    a = loader.load(f16_path, "dec.qkv")
+    b = loader.load(q8_path, "dec.qkv")
+    q.sync()
+    assert torch.equal(a._keep[0], b._keep[0].view(torch.uint8).reshape(-1))
+    assert torch.equal(a._keep[1], b._keep[1].reshape(-1))
+    x = rng.standard_normal(k).astype(np.float32)
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    q.kGemvQ8(out, dev(x), a, n, k)
+    q.sync()
+    assert normwise(out.cpu().numpy(), O.q8_gemv(x, rq, rs, threads=8)) <= 1e-5
