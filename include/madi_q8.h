@@ -183,6 +183,21 @@ int madi_q8_gemv_f16x(float *out, const void *x_f16, const void *qs, const void 
 int madi_q8_pproj(float *out, const float *in, const void *qs, const void *scales,
                   uint32_t m, uint32_t n, uint32_t k);
 
+/* ---- plain fp16 GEMMs (pre-dequantised F16 weights) ------------------------ */
+/* C[M][N] (f16) = epi(A[M][K] (f16) . B[K][N] (f16)), all row-major, fp32
+ * accumulation.  Replaces kM4 / kM4Bias (engine/metal/encoder.zig:125-136) ->
+ * m4_gemm_nn / m4_gemm_bias / m4_gemm_bias_gelu (kernels/m4_gemm.metal:19-115)
+ * for callers that hold an F16 weight in the [K][N] layout kDeq produces.
+ * Epilogues round like the reference: c = f16(A.B), then f16(c + bias[n]) and
+ * for BIAS_GELU f16(gelu(c + bias[n])).  Runs as a library GEMM (rocBLAS). */
+int madi_f16_gemm(const void *a, const void *b, void *c, const float *bias, uint32_t m,
+                  uint32_t n, uint32_t k, int epilogue);
+/* C = alpha * A . B + beta * C, f16 row-major [M][K] . [K][N] -> [M][N], fp32
+ * accumulation.  Replaces mtl_matmul_f16_enc (engine/metal/metal_backend.h:103),
+ * behind matmulF16Batched (metal_backend.zig:120). */
+int madi_matmul_f16(const void *a, const void *b, void *c, int m, int n, int k, float alpha,
+                    float beta);
+
 /* Q8 embedding rows from the panel layout (the tied tok_emb the logit GEMV
  * reads): out[d] = f32(q) * f32(s) for row *tok_ptr (gpu_emb_lookup_q8,
  * graph_helpers.metal:370-383) or row tokens[*pos_ptr]

@@ -54,6 +54,8 @@ SIGNATURES = {
     "madi_q8_logit_gemv": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_gemv_f16x": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _I]),
     "madi_q8_pproj": (_I, [_P, _P, _P, _P, _U32, _U32, _U32]),
+    "madi_f16_gemm": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _I]),
+    "madi_matmul_f16": (_I, [_P, _P, _P, _I, _I, _I, ctypes.c_float, ctypes.c_float]),
     "madi_q8_emb_lookup": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_emb_lookup_indirect": (_I, [_P, _P, _P, _P, _P, _U32, _U32]),
 }

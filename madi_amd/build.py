@@ -56,7 +56,8 @@ def build(verbose: bool = False, extra_flags=(), out: str = LIB, obj_dir: str = 
             print(msg)
         objs.append(obj)
     tmp = out + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs,
+          "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"])
     os.replace(tmp, out)
     return out
 

@@ -19,6 +19,8 @@ hipStream_t stream();
 // `counters` arrival counters that are zero whenever no kernel is using them.
 // Grows on demand (a grow waits for the device); freed by madi_cleanup.
 int workspace(size_t partial_bytes, size_t counters, float **partials, uint32_t **cnt);
+// Releases the fp16 GEMM's rocBLAS handle (madi_cleanup).
+void f16gemm_cleanup();
 
 inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 

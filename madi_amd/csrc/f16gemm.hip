@@ -1,0 +1,103 @@
+// f16gemm.hip -- the boundary's plain fp16 GEMMs on pre-dequantised weights.
+//
+// The engine keeps F16 GEMM entry points for callers that hold an F16 weight
+// (the encoder's F16 cache, the batched decode's WF16 copy): kM4 / kM4Bias
+// (engine/metal/encoder.zig:125-136 -> m4_gemm_nn / m4_gemm_bias /
+// m4_gemm_bias_gelu, kernels/m4_gemm.metal:19-115) and matmulF16Batched
+// (metal_backend.zig:120 -> mtl_matmul_f16_enc, metal_backend.h:103).  These
+// are plain library GEMMs: rocBLAS gemm_ex with f16 operands and fp32
+// accumulation, on the library's stream.  The bias epilogues follow the
+// reference's kernels, which round the product to f16 first and then add the
+// f32 bias (and apply GELU) in one elementwise pass over the f16 result.
+#include <rocblas/rocblas.h>
+
+#include "common.h"
+
+namespace madi {
+
+namespace {
+rocblas_handle g_blas = nullptr;
+
+int blas(rocblas_handle *h, const char *what) {
+  if (!g_blas && rocblas_create_handle(&g_blas) != rocblas_status_success) {
+    g_blas = nullptr;
+    return fail(MADI_ERR_INIT, "%s: rocblas_create_handle failed", what);
+  }
+  if (rocblas_set_stream(g_blas, stream()) != rocblas_status_success)
+    return fail(MADI_ERR_DISPATCH, "%s: rocblas_set_stream failed", what);
+  *h = g_blas;
+  return MADI_OK;
+}
+
+// C[M][N] = alpha * A[M][K] . B[K][N] + beta * C, all row-major f16: the
+// column-major product C^T = B^T A^T with the operands as stored.
+int gemm_f16(const char *what, const void *a, const void *b, void *c, uint32_t m, uint32_t n,
+             uint32_t k, float alpha, float beta) {
+  rocblas_handle h;
+  if (int rc = blas(&h, what)) return rc;
+  const rocblas_status st = rocblas_gemm_ex(
+      h, rocblas_operation_none, rocblas_operation_none, (rocblas_int)n, (rocblas_int)m,
+      (rocblas_int)k, &alpha, b, rocblas_datatype_f16_r, (rocblas_int)n, a, rocblas_datatype_f16_r,
+      (rocblas_int)k, &beta, c, rocblas_datatype_f16_r, (rocblas_int)n, c, rocblas_datatype_f16_r,
+      (rocblas_int)n, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (st != rocblas_status_success)
+    return fail(MADI_ERR_DISPATCH, "%s: rocblas_gemm_ex failed (%s)", what, rocblas_status_to_string(st));
+  return MADI_OK;
+}
+
+// c[r][col] = f16(epi(float(c[r][col]) + bias[col])), m4_gemm.metal:79-85 / 108-114
+template <bool GELU>
+__global__ __launch_bounds__(256) void bias_epilogue_kernel(f16 *__restrict__ c,
+                                                            const float *__restrict__ bias,
+                                                            uint32_t n, size_t count) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  float v = (float)c[i] + bias[i % n];
+  if constexpr (GELU) v = gelu_erf(v);
+  c[i] = (f16)v;
+}
+}  // namespace
+
+void f16gemm_cleanup() {
+  if (g_blas) (void)rocblas_destroy_handle(g_blas);
+  g_blas = nullptr;
+}
+
+}  // namespace madi
+
+using namespace madi;
+
+extern "C" int madi_f16_gemm(const void *a, const void *b, void *c, const float *bias, uint32_t m,
+                             uint32_t n, uint32_t k, int epilogue) {
+  if (!a || !b || !c) return fail(MADI_ERR_NULL, "madi_f16_gemm: null pointer");
+  if (epilogue != MADI_EPI_NONE && epilogue != MADI_EPI_BIAS && epilogue != MADI_EPI_BIAS_GELU)
+    return fail(MADI_ERR_ARG, "madi_f16_gemm: unknown epilogue %d", epilogue);
+  if (epilogue != MADI_EPI_NONE && !bias) return fail(MADI_ERR_NULL, "madi_f16_gemm: null bias");
+  if (m == 0 || n == 0 || k == 0 || m > 0x7fffffffu || n > 0x7fffffffu || k > 0x7fffffffu)
+    return fail(MADI_ERR_SHAPE, "madi_f16_gemm: m=%u n=%u k=%u", m, n, k);
+  if (!aligned(a, 2) || !aligned(b, 2) || !aligned(c, 2) || (bias && !aligned(bias, 4)))
+    return fail(MADI_ERR_ALIGN, "madi_f16_gemm: misaligned operand");
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_f16_gemm: madi_init has not succeeded");
+  if (int rc = gemm_f16("madi_f16_gemm", a, b, c, m, n, k, 1.0f, 0.0f)) return rc;
+  if (epilogue == MADI_EPI_NONE) return MADI_OK;
+  const size_t count = (size_t)m * n;
+  const dim3 grid((unsigned)((count + 255) / 256));
+  if (epilogue == MADI_EPI_BIAS)
+    hipLaunchKernelGGL(bias_epilogue_kernel<false>, grid, dim3(256), 0, stream(),
+                       static_cast<f16 *>(c), bias, n, count);
+  else
+    hipLaunchKernelGGL(bias_epilogue_kernel<true>, grid, dim3(256), 0, stream(),
+                       static_cast<f16 *>(c), bias, n, count);
+  return check_launch("madi_f16_gemm(epilogue)");
+}
+
+extern "C" int madi_matmul_f16(const void *a, const void *b, void *c, int m, int n, int k,
+                               float alpha, float beta) {
+  if (!a || !b || !c) return fail(MADI_ERR_NULL, "madi_matmul_f16: null pointer");
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail(MADI_ERR_SHAPE, "madi_matmul_f16: m=%d n=%d k=%d", m, n, k);
+  if (!aligned(a, 2) || !aligned(b, 2) || !aligned(c, 2))
+    return fail(MADI_ERR_ALIGN, "madi_matmul_f16: misaligned operand");
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_matmul_f16: madi_init has not succeeded");
+  return gemm_f16("madi_matmul_f16", a, b, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, alpha, beta);
+}

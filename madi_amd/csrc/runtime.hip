@@ -110,6 +110,7 @@ extern "C" void madi_cleanup(void) {
   if (!g_init) return;
   (void)hipStreamSynchronize(g_stream);
   free_workspace();
+  f16gemm_cleanup();
   g_stream = nullptr;
   g_init = false;
 }

@@ -149,6 +149,24 @@ def kGemmQ8Bias(a, w: Q8, c, bias, m: int, n: int, k: int, gelu: bool = False) -
          EPI_BIAS_GELU if gelu else EPI_BIAS)
 
 
+def kM4(a, b, c, m: int, n: int, k: int) -> None:
+    """encoder.zig:125-130 (m4_gemm_nn): C = A . B, f16 [M][K] . [K][N] (an F16
+    weight, e.g. the output of kDeq)."""
+    call("madi_f16_gemm", ptr(a), ptr(b), ptr(c), None, m, n, k, EPI_NONE)
+
+
+def kM4Bias(a, b, c, bias, m: int, n: int, k: int, gelu: bool = False) -> None:
+    """encoder.zig:131-136 (m4_gemm_bias / m4_gemm_bias_gelu)."""
+    call("madi_f16_gemm", ptr(a), ptr(b), ptr(c), ptr(bias), m, n, k,
+         EPI_BIAS_GELU if gelu else EPI_BIAS)
+
+
+def matmulF16Batched(a, b, c, m: int, n: int, k: int, alpha: float = 1.0,
+                     beta: float = 0.0) -> None:
+    """metal_backend.zig:120 -> mtl_matmul_f16_enc (metal_backend.h:103)."""
+    call("madi_matmul_f16", ptr(a), ptr(b), ptr(c), m, n, k, alpha, beta)
+
+
 # ---- decoder.zig -----------------------------------------------------------
 def kGemvQ8(out, x, w: Q8, n: int, k: int) -> None:
     """decoder.zig:155-160 (gemv_q8)."""
@@ -204,7 +222,7 @@ def gemv_f16x(out, x16, w: Q8, n: int, k: int, bias=None, epilogue: int = EPI_NO
 
 __all__ = [
     "D", "MLP", "VOCAB", "ENC_SEQ", "Q8", "init", "sync", "repack_host", "unpack_host",
-    "upload_q8", "upload_q8_device_repack", "quantize", "fnv", "FNV_SEED", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias",
+    "upload_q8", "upload_q8_device_repack", "quantize", "fnv", "FNV_SEED", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias", "kM4", "kM4Bias", "matmulF16Batched",
     "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "pproj", "kQkv", "kLogitGemv", "embLookup",
     "embLookupIndirect", "gemv_f16x", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU",
     "EPI_BIAS_RES",

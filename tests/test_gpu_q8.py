@@ -472,3 +472,55 @@ def test_q8_file_load_equals_f16_quantize(q, tmp_path):
     q.kGemvQ8(out, dev(x), a, n, k)
     q.sync()
     assert normwise(out.cpu().numpy(), O.q8_gemv(x, rq, rs, threads=8)) <= 1e-5
+
+
+# ------------------------------------------------------------------ plain fp16 GEMMs (F16 weights)
+@pytest.mark.parametrize("m,n,k", [(50, 64, 96), (8, 3840, 1280), (300, 1280, 1280)])
+def test_matmul_f16_alpha_beta(q, m, n, k):
+    """mtl_matmul_f16_enc semantics, C = alpha A.B + beta C, against the
+    oracle's restatement; MPS's accumulation order is undocumented, so the bar
+    is the fp32-accumulation + f16-rounding bound, not bits."""
+    say(f"matmul_f16 m={m} n={n} k={k}")
+    rng = np.random.default_rng(m + n)
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    b = (rng.standard_normal((k, n)) * 0.05).astype(np.float16)
+    c0 = rng.standard_normal((m, n)).astype(np.float16)
+    for alpha, beta in ((1.0, 0.0), (0.5, 2.0)):
+        dc = dev_f16(c0)
+        q.matmulF16Batched(dev_f16(a), dev_f16(b), dc, m, n, k, alpha, beta)
+        q.sync()
+        got = host_f16(dc).astype(np.float64)
+        ref = O.gemm_f16(a, b, c=c0, alpha=alpha, beta=beta, threads=8).astype(np.float64)
+        assert normwise(got, ref) <= TOL
+        exact = alpha * (a.astype(np.float64) @ b.astype(np.float64)) + beta * c0.astype(np.float64)
+        bound = 2.0**-11 * np.abs(exact) + (k + 2) * 2.0**-24 * (
+            abs(alpha) * (np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64)))
+            + abs(beta) * np.abs(c0.astype(np.float64))) + 2.0**-24
+        assert np.all(np.abs(got - exact) <= bound * 1.001)
+
+
+@pytest.mark.parametrize("epi", [O.EPI_NONE, O.EPI_BIAS, O.EPI_BIAS_GELU])
+def test_f16_gemm_kM4_epilogues(q, epi):
+    """kM4 / kM4Bias on an F16 weight produced by kDeq from a Q8 weight: the
+    product is rounded to f16 before the bias (m4_gemm.metal:79-85), which
+    composes the oracle's f16 GEMM, f32->f16 rounding and GELU."""
+    m, n, k = 96, 512, 1280
+    a, qs, sc = synth.gemm_case(77, m, n, k)
+    w16 = O.dequant_q8_f16(qs, sc)  # [K][N]
+    bias = np.random.default_rng(78).standard_normal(n).astype(np.float32)
+    dc = torch.empty((m, n), dtype=torch.int16, device="cuda")
+    if epi == O.EPI_NONE:
+        q.kM4(dev_f16(a), dev_f16(w16), dc, m, n, k)
+    else:
+        q.kM4Bias(dev_f16(a), dev_f16(w16), dc, dev(bias), m, n, k, gelu=epi == O.EPI_BIAS_GELU)
+    q.sync()
+    got = host_f16(dc).astype(np.float64)
+    c16 = O.gemm_f16(a, w16, threads=8)
+    if epi == O.EPI_NONE:
+        ref = c16.astype(np.float64)
+    else:
+        v = c16.astype(np.float32) + bias[None, :]
+        if epi == O.EPI_BIAS_GELU:
+            v = np.vectorize(O.gelu_erf, otypes=[np.float32])(v)
+        ref = O.f32_to_f16(v).astype(np.float64)
+    assert normwise(got, ref) <= TOL
