@@ -197,6 +197,21 @@ def test_gemm_encoder_shapes_full_m(q, name, n, k):
     assert np.all(np.isfinite(c))
 
 
+def test_gemm_large_m(q):
+    """Several tiles per CU (M = 6657: 53 x 20 tiles of 128 x 256, a 1-row M
+    tail); row sample over tile boundaries."""
+    m, n, k = 6657, 5120, 1280
+    say(f"gemm large m={m} n={n} k={k}")
+    a, qs, sc = synth.gemm_case(9, m, n, k)
+    c = _gemm(q, a, qs, sc)
+    rows = np.unique(np.r_[0, 31, 32, 255, 256, 257, 511, 512, 4095, 4096, 6400, 6655, 6656,
+                           np.random.default_rng(2).integers(0, m, 12)])
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, threads=16)
+    assert normwise(c[rows], ref) <= TOL
+    assert tight_ok(c[rows], a[rows], qs, sc)
+    assert np.all(np.isfinite(c))
+
+
 # ------------------------------------------------------------------ GEMV
 @pytest.mark.parametrize("n,k", [(51866, 1280), (3840, 1280), (1280, 5120), (5120, 1280), (40, 64)])
 def test_gemv_parity(q, n, k):
