@@ -52,6 +52,11 @@ struct GemvArgs {
   const float *qb, *vb;
   float *kc, *vc;
   const uint32_t *pos;
+  // split K over `splits` workgroups per panel: partial row sums in `ws`
+  // ([panel][split][32]), arrival counters in `cnt` ([panel], zero between uses)
+  uint32_t splits;
+  float *ws;
+  uint32_t *cnt;
 };
 
 // LDS bytes: x (K elements of XT), the wave partials
@@ -141,10 +146,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
-  const uint32_t p = blockIdx.x;
+  const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
+  const uint32_t p = blockIdx.x % np, split = blockIdx.x / np;
   const uint32_t R = panel_rows(a.n, p);
   const bool live = r < R;
-  const uint32_t c0 = (wave * C) / kWaves, c1 = ((wave + 1) * C) / kWaves;
+  // this workgroup's K chunks [cs, ce), split four ways over the waves
+  const uint32_t cs = split * C / a.splits, ce = (split + 1) * C / a.splits;
+  const uint32_t c0 = cs + (wave * (ce - cs)) / kWaves, c1 = cs + ((wave + 1) * (ce - cs)) / kWaves;
 
   // ---- x: load first (16 bytes per thread and piece), then the weights.
   // Lanes past a partial panel's last row read row R-1 (in bounds; their sums
@@ -190,9 +198,33 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   acc += __shfl_xor(acc, 32);
   if (h == 0) red[wave * 32 + r] = acc;
   __syncthreads();
-  if (threadIdx.x >= R) return;
-  const float v = red[threadIdx.x] + red[32 + threadIdx.x] + red[64 + threadIdx.x] + red[96 + threadIdx.x];
-  const uint32_t nrow = p * kPanelRows + threadIdx.x;
+  const uint32_t t = threadIdx.x;
+  float v = 0.0f;
+  if (t < 32) v = red[t] + red[32 + t] + red[64 + t] + red[96 + t];
+  if (a.splits > 1) {
+    // Split K: each workgroup writes its 32 partial row sums through to memory
+    // (system-scope stores) and counts itself in; the last to arrive adds the
+    // splits' partials in split order (the same order whoever arrives last)
+    // and stores the rows.
+    __shared__ uint32_t arrived;
+    float *mine = a.ws + ((size_t)p * a.splits + split) * 32;
+    if (t < 32) __hip_atomic_store(mine + t, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (t == 0)
+      arrived = __hip_atomic_fetch_add(&a.cnt[p], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+    if (arrived != a.splits - 1) return;
+    if (t < 32) {
+      const float *all = a.ws + (size_t)p * a.splits * 32 + t;
+      v = 0.0f;
+      for (uint32_t s2 = 0; s2 < a.splits; ++s2)
+        v += __hip_atomic_load(all + s2 * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+    if (t == 0) __hip_atomic_store(&a.cnt[p], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+  if (t >= R) return;
+  const uint32_t nrow = p * kPanelRows + t;
   if constexpr (MODE == kPlain) {
     a.out[nrow] = v;
   } else if constexpr (MODE == kBias) {
@@ -223,9 +255,18 @@ int launch(const char *what, const GemvArgs &a) {
   if (!aligned(a.qs, 16) || !aligned(a.sc, 2) || !aligned(a.x, 16))
     return fail(MADI_ERR_ALIGN, "%s: qs and x need 16-byte alignment", what);
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);
-  const uint32_t grid = (a.n + kPanelRows - 1) / kPanelRows;
+  const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows, C = a.k / kChunkK;
+  // Few panels and a long K (the 5120-wide FFN down projection: 40 panels)
+  // leave most CUs idle and each wave with a long chain of loads: split K
+  // over up to four workgroups per panel, >= 16 chunks each.
+  GemvArgs b = a;
+  b.splits = 1;
+  if (np < 128 && C >= 32) {
+    b.splits = C / 16 < 4 ? C / 16 : 4;
+    if (int rc = workspace((size_t)np * b.splits * 32 * 4, np, &b.ws, &b.cnt)) return rc;
+  }
   const size_t lds = lds_bytes<XT>(a.k);
-  hipLaunchKernelGGL((q8_gemv_kernel<XT, MODE>), dim3(grid), dim3(256), lds, stream(), a);
+  hipLaunchKernelGGL((q8_gemv_kernel<XT, MODE>), dim3(np * b.splits), dim3(256), lds, stream(), b);
   return check_launch(what);
 }
 

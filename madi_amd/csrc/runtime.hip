@@ -102,6 +102,15 @@ extern "C" int madi_init(void) {
                 prop.gcnArchName);
   g_cu_count = prop.multiProcessorCount;
   g_init = true;
+  // A workspace big enough for every split GEMV / projection (and small
+  // split GEMMs) from the start, so those never allocate later (e.g. while a
+  // caller captures a graph).
+  float *partials = nullptr;
+  uint32_t *cnt = nullptr;
+  if (int rc = workspace(size_t(4) << 20, kCounters, &partials, &cnt)) {
+    g_init = false;
+    return rc;
+  }
   g_err[0] = 0;
   return MADI_OK;
 }

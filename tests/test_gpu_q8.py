@@ -272,9 +272,9 @@ def test_logit_gemv_vocab(q):
     assert int(np.argmax(got)) == int(np.argmax(ref))
 
 
+@pytest.mark.parametrize("n,k", [(5120, 1280), (1280, 5120)])  # the second splits K over workgroups
 @pytest.mark.parametrize("epi", ["bias", "gemv_q8_bias_gelu", "gemv_q8_bias_res"])
-def test_gemv_epilogues(q, epi):
-    n, k = 5120, 1280
+def test_gemv_epilogues(q, epi, n, k):
     x16, qs, sc = synth.gemv_case(7, n, k)
     x = x16.astype(np.float32)
     rng = np.random.default_rng(8)
