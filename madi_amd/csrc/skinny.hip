@@ -122,6 +122,11 @@ struct SkinnyArgs {
   const f16 *sc;
   uint32_t m, n, k;
   uint32_t groups, slices;  // panel groups (P panels each) and 32-row activation slices
+  // split K over `splits` workgroups per (group, slice): partial tiles in `ws`,
+  // arrival counters in `cnt` (zero between uses)
+  uint32_t splits;
+  f32x4 *ws;
+  uint32_t *cnt;
 };
 
 // LDS: the four waves' activation tiles during the K loop, then the partial
@@ -140,8 +145,9 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   // Consecutive workgroups go to different XCDs (round-robin).  Map the
   // slices of one panel group to one XCD so they share its weights in that
   // L2: workgroup b runs on XCD b % 8 and takes group 8 * ((b / 8) / S) + b % 8,
-  // slice (b / 8) % S.
-  const uint32_t b = blockIdx.x, S = a.slices;
+  // slice (b / 8) % S; split K ranges are the slowest index.
+  const uint32_t per_split = (a.groups + 7) / 8 * 8 * a.slices;
+  const uint32_t split = blockIdx.x / per_split, b = blockIdx.x % per_split, S = a.slices;
   const uint32_t grp = 8 * ((b / 8) / S) + b % 8, slice = (b / 8) % S;
   if (grp >= a.groups) return;
 
@@ -150,7 +156,9 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
   const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
-  const uint32_t c0 = (wave * C) / KW, c1 = ((wave + 1) * C) / KW;
+  // this workgroup's K chunks [cs, ce), split KW ways over the waves
+  const uint32_t cs = split * C / a.splits, ce = (split + 1) * C / a.splits;
+  const uint32_t c0 = cs + (wave * (ce - cs)) / KW, c1 = cs + ((wave + 1) * (ce - cs)) / KW;
 
   // Panels past N are clamped to the last one and lanes past a partial
   // panel's last row read row R-1 (in bounds; their sums are never stored).
@@ -205,26 +213,67 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
       red[((wave * P + t) * 4 + g) * 64 + lane] =
           (f32x4){acc[t][4 * g], acc[t][4 * g + 1], acc[t][4 * g + 2], acc[t][4 * g + 3]};
   __syncthreads();
+  f32x4 v[P];
+  if (wave < 4) {
+#pragma unroll
+    for (int t = 0; t < P; ++t) {
+      v[t] = red[((0 * P + t) * 4 + wave) * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < KW; ++w) v[t] += red[((w * P + t) * 4 + wave) * 64 + lane];
+    }
+  }
+  if (a.splits > 1) {
+    // Split K: each workgroup writes its partial tile through to memory
+    // (device-scope sc1 stores) and counts itself in; the last to arrive adds
+    // the splits' partials in split order and stores the rows.
+    __shared__ uint32_t arrived;
+    constexpr int kSc1 = 16;
+    const uint32_t tile = grp * a.slices + slice;
+    const uint32_t part = P * 4 * 64 * 16;  // bytes per partial tile
+    const __amdgpu_buffer_rsrc_t wsr = make_rsrc(a.ws, a.groups * a.slices * a.splits * part);
+    if (wave < 4) {
+#pragma unroll
+      for (int t = 0; t < P; ++t)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[t]), wsr,
+                                               ((t * 4 + wave) * 64 + lane) * 16,
+                                               (tile * a.splits + split) * part, kSc1);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0)
+      arrived = __hip_atomic_fetch_add(&a.cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    __syncthreads();
+    if (arrived != a.splits - 1) return;
+    if (wave < 4) {
+#pragma unroll
+      for (int t = 0; t < P; ++t) {
+        v[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
+        for (uint32_t s2 = 0; s2 < a.splits; ++s2)
+          v[t] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                wsr, ((t * 4 + wave) * 64 + lane) * 16,
+                                                (tile * a.splits + s2) * part, kSc1));
+      }
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_store(&a.cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
   const uint32_t m = m0 + r;
   if (wave >= 4 || m >= a.m) return;
   const uint32_t nl = wave * 8 + h * 4;  // panel-local row of v.x
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     if (grp * P + t >= np) break;
-    f32x4 v = red[((0 * P + t) * 4 + wave) * 64 + lane];
-#pragma unroll
-    for (int w = 1; w < KW; ++w) v += red[((w * P + t) * 4 + wave) * 64 + lane];
     const uint32_t R = pl.R[t];
     float *o = a.out + (size_t)m * a.n + pl.p[t] * kPanelRows + nl;
     if (nl + 4 <= R) {
-      o[0] = v.x;
-      o[1] = v.y;
-      o[2] = v.z;
-      o[3] = v.w;
+      o[0] = v[t].x;
+      o[1] = v[t].y;
+      o[2] = v[t].z;
+      o[3] = v[t].w;
     } else {
-      if (nl + 0 < R) o[0] = v.x;
-      if (nl + 1 < R) o[1] = v.y;
-      if (nl + 2 < R) o[2] = v.z;
+      if (nl + 0 < R) o[0] = v[t].x;
+      if (nl + 1 < R) o[1] = v[t].y;
+      if (nl + 2 < R) o[2] = v[t].z;
     }
   }
 }
@@ -233,7 +282,19 @@ template <int P, int KW, int WPE>
 int launch_skinny(SkinnyArgs a) {
   const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
   a.groups = (np + P - 1) / P;
-  const uint32_t grid = (a.groups + 7) / 8 * 8 * a.slices;
+  const uint32_t C = a.k / kChunkK;
+  // Few panels and a long K (the FFN down projection, 40 panels x 80 chunks):
+  // split K over up to four workgroups per tile, >= 16 chunks each.
+  a.splits = 1;
+  if (P == 1 && np < 128 && C >= 32) {
+    a.splits = C / 16 < 4 ? C / 16 : 4;
+    float *ws = nullptr;
+    const size_t part = (size_t)P * 4 * 64 * 16;
+    if (int rc = workspace(a.groups * a.slices * a.splits * part, a.groups * a.slices, &ws, &a.cnt))
+      return rc;
+    a.ws = reinterpret_cast<f32x4 *>(ws);
+  }
+  const uint32_t grid = (a.groups + 7) / 8 * 8 * a.slices * a.splits;
   hipLaunchKernelGGL((q8_skinny_kernel<P, KW, WPE>), dim3(grid), dim3(KW * 64), 0, stream(), a);
   return check_launch("madi_q8_pproj");
 }
