@@ -115,19 +115,37 @@ __device__ inline desc_t make_desc(const void *base, uint32_t bytes) {
   return (desc_t){(uint32_t)b, (uint32_t)(b >> 32) & 0xffffu, bytes, 0x00020000u};
 }
 
-// 16 bytes per lane at soff + voff into VGPRs.
+// The scalar offset operand of a buffer access.  Offsets are uniform, but the
+// compiler may compute one on the vector ALU (e.g. a clamp it folds into a
+// vector compare); readfirstlane returns it to an SGPR and costs nothing when
+// it is already there.
+__device__ inline uint32_t sgpr(uint32_t x) { return __builtin_amdgcn_readfirstlane(x); }
+
+// 16 bytes per lane at soff + voff + OFF into VGPRs.
+template <int OFF = 0>
 __device__ inline void vload16(u32x4 &v, desc_t d, uint32_t voff, uint32_t soff) {
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff));
+  static_assert(OFF >= 0 && OFF < 4096, "instruction offset range");
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen offset:%4"
+               : "=v"(v) : "v"(voff), "s"(d), "s"(sgpr(soff)), "n"(OFF));
 }
 // 2 bytes per lane (zero-extended) at soff + voff into a VGPR.
 __device__ inline void vload2(uint32_t &v, desc_t d, uint32_t voff, uint32_t soff) {
-  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(d), "s"(soff));
+  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen"
+               : "=v"(v) : "v"(voff), "s"(d), "s"(sgpr(soff)));
 }
-// One wave-wide DMA of 16 bytes per lane: buffer bytes [soff + voff, +16) ->
-// LDS lds + 16*lane.
-__device__ inline void dma16(desc_t d, uint32_t voff, uint32_t soff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               ::"s"(lds), "v"(voff), "s"(d), "s"(soff) : "memory", "m0");
+// One wave-wide DMA of 16 bytes per lane: buffer bytes [soff + voff + OFF,
+// +16) -> LDS m0 + OFF + 16*lane (the instruction offset moves both
+// addresses), so one M0 value serves all of a chunk's DMAs.  The first DMA
+// after M0 changes waits the one state an M0 write needs before an LDS DMA.
+template <int OFF, bool FIRST>
+__device__ inline void dma16(desc_t d, uint32_t voff, uint32_t soff, uint32_t m0) {
+  static_assert(OFF >= 0 && OFF < 4096, "instruction offset range");
+  if constexpr (FIRST)
+    asm volatile("s_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen offset:%3 lds"
+                 ::"v"(voff), "s"(d), "s"(sgpr(soff)), "n"(OFF), "{m0}"(sgpr(m0)) : "memory");
+  else
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen offset:%3 lds"
+                 ::"v"(voff), "s"(d), "s"(sgpr(soff)), "n"(OFF), "{m0}"(sgpr(m0)) : "memory");
 }
 #pragma clang diagnostic pop
 
@@ -170,31 +188,44 @@ struct Plan {
   desc_t wq, ws, wa, zero;  // weights, scales, activations, empty
   uint32_t w_soff[2];       // byte offset of panel (2*wave + t) in the weights
   uint32_t s_voff[2];       // per-lane byte offset of this lane's scale, panel t
-  uint32_t a_voff[MT];      // per-lane activation offsets of the wave's row groups
+  uint32_t a_voff[MT];      // per-lane activation offsets of the wave's row groups,
+                            // less the DMA's instruction offset (1024 * group)
+  uint32_t a_lds;           // the wave's first row group within an A stage
   uint32_t nchunks;
 };
 
+// Row-group DMA I of the wave's A tile for one chunk.
+template <int MT, int I>
+__device__ inline void dma_group(desc_t wa, const Plan<MT> &p, uint32_t c, uint32_t m0) {
+  dma16<I * 1024, I == 0>(wa, p.a_voff[I], c * 128, m0);
+}
+
 // The vector-memory issues of k-step s for chunk c's A stage (into `slot`) and
-// chunk cw's weights (into `w`); chunks past the last one load zeros.
+// chunk cw's weights (into `w`); chunks past the last one load zeros (an empty
+// descriptor touches no memory).
 template <int MT>
 __device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, uint32_t cw,
-                                   const Plan<MT> &p, uint32_t wave, uint32_t lane) {
+                                   const Plan<MT> &p, uint32_t lane) {
   const desc_t wa = c < p.nchunks ? p.wa : p.zero;
   const bool live = cw < p.nchunks;
   const desc_t wq = live ? p.wq : p.zero, ws = live ? p.ws : p.zero;
-  const uint32_t base = lds_addr(slot);
+  const uint32_t m0 = lds_addr(slot) + p.a_lds;
   if (s == 0) {
-#pragma unroll
-    for (int i = 0; i < MT / 2; ++i) dma16(wa, p.a_voff[i], c * 128, base + (wave + 4 * i) * 1024);
+    if constexpr (MT >= 2) dma_group<MT, 0>(wa, p, c, m0);
+    if constexpr (MT >= 4) dma_group<MT, 1>(wa, p, c, m0);
   } else if (s == 1) {
-#pragma unroll
-    for (int i = MT / 2; i < MT; ++i) dma16(wa, p.a_voff[i], c * 128, base + (wave + 4 * i) * 1024);
+    if constexpr (MT == 1) dma_group<MT, 0>(wa, p, c, m0);
+    if constexpr (MT == 2) dma_group<MT, 1>(wa, p, c, m0);
+    if constexpr (MT == 4) {
+      dma_group<MT, 2>(wa, p, c, m0);
+      dma_group<MT, 3>(wa, p, c, m0);
+    }
     vload16(w.u[0][0], wq, lane * 16, p.w_soff[0] + cw * 2048);
   } else if (s == 2) {
-    vload16(w.u[0][1], wq, lane * 16, p.w_soff[0] + cw * 2048 + 1024);
+    vload16<1024>(w.u[0][1], wq, lane * 16, p.w_soff[0] + cw * 2048);
     vload16(w.u[1][0], wq, lane * 16, p.w_soff[1] + cw * 2048);
   } else {
-    vload16(w.u[1][1], wq, lane * 16, p.w_soff[1] + cw * 2048 + 1024);
+    vload16<1024>(w.u[1][1], wq, lane * 16, p.w_soff[1] + cw * 2048);
     vload2(w.s[0], ws, p.s_voff[0], cw * 128);
     vload2(w.s[1], ws, p.s_voff[1], cw * 128);
   }
@@ -221,6 +252,14 @@ __device__ inline f16x8 dequant_frag(const RawW &w, int t, int s) {
   return (f16x8){a0.x, a0.y, a1.x, a1.y, a2.x, a2.y, a3.x, a3.y};
 }
 
+// s_waitcnt lgkmcnt(0) with vmcnt and expcnt left at their maxima (gfx9
+// encoding: vmcnt bits 15:14 and 3:0, expcnt 6:4, lgkmcnt 11:8)
+constexpr int kLgkm0 = 0xC07F;
+
+// Buffer cache policy sc1: the access writes through (stores) or reads past
+// (loads) the XCD's own L2.
+constexpr int kSc1 = 16;
+
 // sched_group_barrier masks
 constexpr int kSchedVALU = 0x002;
 constexpr int kSchedMFMA = 0x008;
@@ -241,16 +280,15 @@ __device__ inline void schedule_step() {
   }
 }
 
-// One chunk c.  On entry w holds chunk c's fragments except w[1][3] (made at
-// step 0 from `cur`, chunk c's weights), `af` holds chunk c's step-0
+// One chunk c.  On entry w holds chunk c's fragments except w[0][3] and
+// w[1][3] (made at step 0 from `cur`, chunk c's weights), `af` holds chunk c's step-0
 // activation fragments, and `nxt` receives chunk c+1's weights (loaded WD-1
 // chunks ago; waited for here).  `ld` (the same
 // register set as `cur`, free after step 0) receives chunk c+WD's weights.
 template <int MT>
-__device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint32_t wave,
-                             uint32_t lane, uint32_t h, uint32_t r, f32x16 (&acc)[2][MT],
-                             f16x8 (&w)[2][4], f16x8 (&af)[MT], const RawW &cur, RawW &nxt,
-                             RawW &ld) {
+__device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint32_t lane,
+                             uint32_t h, uint32_t r, f32x16 (&acc)[2][MT], f16x8 (&w)[2][4],
+                             f16x8 (&af)[MT], const RawW &cur, RawW &nxt, RawW &ld) {
   using G = Geometry<MT>;
   const uint8_t *At = smem + (c % NA) * G::kStage;
   const uint8_t *An = smem + ((c + 1) % NA) * G::kStage;
@@ -258,7 +296,11 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint3
   wait_weights<G::kVmRaw>(nxt);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    if (s == 3) wait_then_barrier<G::kVmA>();  // chunk c+1's A stage is visible
+    // the previous step's fragment reads (issued a whole step ago) have
+    // landed: one wait here instead of one before each MFMA
+    if (s == 3)
+      wait_then_barrier<G::kVmA>();  // chunk c+1's A stage is visible
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
     f16x8 an[MT];
     if (s < 3)
       load_a_frags<MT>(At, s + 1, h, r, an);
@@ -267,13 +309,15 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint3
 #pragma unroll
     for (int i = 0; i < MT; ++i)
       acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[0][s], af[i], acc[0][i], 0, 0, 0);
-    // panel 1's step s-1 fragment was consumed last step: refill it
-    w[1][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 1, (s + 3) & 3);
+    // each panel's step s-1 fragment was consumed last step, at least 2*MT
+    // MFMAs before its refill here (no read-after-write wait states): its
+    // next value is chunk c's own step-3 fragment at step 0, else chunk c+1's
+    w[0][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 0, (s + 3) & 3);
 #pragma unroll
     for (int i = 0; i < MT; ++i)
       acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[1][s], af[i], acc[1][i], 0, 0, 0);
-    w[0][s] = dequant_frag(nxt, 0, s);
-    issue_loads<MT>(s, Af, c + NA - 1, ld, c + WD, p, wave, lane);
+    w[1][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 1, (s + 3) & 3);
+    issue_loads<MT>(s, Af, c + NA - 1, ld, c + WD, p, lane);
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[i] = an[i];
     schedule_step<MT>();
@@ -336,12 +380,16 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   }
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
-    const uint32_t row = (wave + 4 * i) * 8 + (lane >> 3);
+    // wave w copies row groups MT*w .. MT*w+MT-1 (8 rows each) of the stage
+    const uint32_t row = (MT * wave + i) * 8 + (lane >> 3);
     const uint32_t q = (lane & 7) ^ a_swz(row);
     uint32_t m = m0 + row;
     m = m < M ? m : M - 1;
-    p.a_voff[i] = m * K * 2 + cb * 128 + q * 16;
+    // the DMA adds its instruction offset 1024*i to both addresses (row group
+    // i starts 8*i rows, at least 1024*i bytes, into A, so this cannot wrap)
+    p.a_voff[i] = m * K * 2 + cb * 128 + q * 16 - 1024 * i;
   }
+  p.a_lds = MT * wave * 1024;
 
   f32x16 acc[2][MT];
 #pragma unroll
@@ -363,14 +411,14 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
     uint8_t *slot = smem + (uint32_t)((j + NA - 1 + NA) % NA) * G::kStage;
     RawW &rw = j == -4 ? r0 : j == -3 ? r1 : j == -2 ? r2 : r3;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) issue_loads<MT>(st, slot, ca, rw, (uint32_t)(j + WD), p, wave, lane);
+    for (int st = 0; st < 4; ++st) issue_loads<MT>(st, slot, ca, rw, (uint32_t)(j + WD), p, lane);
   }
   // chunk 0's weights and A stage, then its fragments
   wait_then_barrier<G::kVmPrologue>();
   wait_weights<G::kVmPrologue>(r0);
   f16x8 w[2][4], af[MT];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) w[0][s] = dequant_frag(r0, 0, s);
+  for (int s = 0; s < 3; ++s) w[0][s] = dequant_frag(r0, 0, s);
 #pragma unroll
   for (int s = 0; s < 3; ++s) w[1][s] = dequant_frag(r0, 1, s);
   load_a_frags<MT>(smem, 0, h, r, af);
@@ -380,10 +428,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   // allocator copy asm-loaded registers before their vmcnt wait.
   const uint32_t cpad = (nchunks + WD - 1) / WD * WD;
   for (uint32_t c = 0; c < cpad; c += 4) {
-    chunk<MT>(smem, p, c + 0, wave, lane, h, r, acc, w, af, r0, r1, r0);
-    chunk<MT>(smem, p, c + 1, wave, lane, h, r, acc, w, af, r1, r2, r1);
-    chunk<MT>(smem, p, c + 2, wave, lane, h, r, acc, w, af, r2, r3, r2);
-    chunk<MT>(smem, p, c + 3, wave, lane, h, r, acc, w, af, r3, r0, r3);
+    chunk<MT>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+    chunk<MT>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+    chunk<MT>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+    chunk<MT>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
   }
 
   // ---- epilogue.  Lane (h, r) holds D[n][m] for m = 32i + r and
@@ -399,7 +447,6 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
     // the XCD's own L2, and the count is a system-scope atomic, so no L2-wide
     // writeback or invalidate is needed.
     constexpr uint32_t kPart = 4 * 2 * MT * 4 * 64 * 16;  // bytes per partial tile
-    constexpr int kSc1 = 16;                             // cache policy: sc1
     const __amdgpu_buffer_rsrc_t wsr =
         __builtin_amdgcn_make_buffer_rsrc(ws, 0, (int)(T * splits * kPart), 0x00020000);
 #pragma unroll
@@ -475,15 +522,20 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   }
   __syncthreads();
   // wave w stores tile rows [8*MT*w, 8*MT*(w+1)), two rows (512 B each) per
-  // instruction: lane (h, r) writes 16 bytes of row 2j + h at column 8r
+  // instruction: lane (h, r) writes 16 bytes of row 2j + h at column 8r.  The
+  // stores write through the L2 (sc1), so the tile leaves no dirty lines for
+  // the end-of-kernel release to write back after the last workgroup; rows
+  // past M fall outside the tile's buffer resource and are dropped.
   const uint32_t n = p0 * kPanelRows + r * 8;
   if (n >= N) return;
+  const uint32_t rows = M - m0 < 32 * MT ? M - m0 : 32 * MT;
+  const __amdgpu_buffer_rsrc_t cr =
+      __builtin_amdgcn_make_buffer_rsrc(Cout + (size_t)m0 * N, 0, (int)(rows * N * 2), 0x00020000);
 #pragma unroll
   for (int j = 0; j < 4 * MT; ++j) {
     const uint32_t row = wave * 8 * MT + 2 * j + h;
-    const uint32_t m = m0 + row;
     const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * kCStride + r * 16);
-    if (m < M) *reinterpret_cast<u32x4 *>(Cout + (size_t)m * N + n) = v;
+    __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * N + n) * 2, 0, kSc1);
   }
 }
 
@@ -539,8 +591,10 @@ extern "C" int madi_q8_gemm(const void *a, const void *qs, const void *scales, v
   if (m == 0 || n == 0 || k == 0 || n % kPanelRows || k % kChunkK)
     return fail(MADI_ERR_SHAPE, "madi_q8_gemm: m=%u n=%u k=%u (need n %% 32 == 0, k %% 64 == 0)", m, n, k);
   // buffer offsets are 32-bit (and buffer sizes below 2 GiB): the operands
-  // A (m*k*2 bytes) and W (n*k bytes) must stay below 2 GiB
-  if ((uint64_t)m * k * 2 >= (1ull << 31) || (uint64_t)n * k >= (1ull << 31))
+  // A (m*k*2 bytes) and W (n*k bytes) and one 128-row C tile (256*n bytes)
+  // must stay below 2 GiB
+  if ((uint64_t)m * k * 2 >= (1ull << 31) || (uint64_t)n * k >= (1ull << 31) ||
+      (uint64_t)n * 256 >= (1ull << 31))
     return fail(MADI_ERR_SHAPE, "madi_q8_gemm: m=%u n=%u k=%u exceeds the 2 GiB operand limit", m, n, k);
   if (!aligned(a, 16) || !aligned(qs, 16) || !aligned(scales, 16) || !aligned(c, 16) ||
       (bias && !aligned(bias, 16)))
