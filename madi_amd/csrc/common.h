@@ -53,16 +53,18 @@ __host__ __device__ inline size_t panel_chunk_sc(uint32_t k, uint32_t p, uint32_
   return (size_t)p * kPanelRows * (k / 32) + (size_t)c * 2 * rows;
 }
 
-// Two biased bytes (q + 128) of `w`, selected by `sel`, to the exact fp16 pair
-// (q0, q1) times the fp16 scale pair `s2`.  The perm builds the fp16 bit
-// patterns 0x64uu = 1024 + u for each byte u, so x - 1152 = q exactly; one IEEE
-// fp16 multiply of the exact operands then gives fp16_rne(q * s), the
-// reference's half(float(q) * float(s)) (q8_gemm.metal:26) bit for bit.
-__device__ inline f16x2 dequant_pair(uint32_t w, uint32_t sel, f16x2 s2) {
-  uint32_t p = __builtin_amdgcn_perm(0x64646464u, w, sel);
-  f16x2 x = __builtin_bit_cast(f16x2, p);
+// q_pair: two biased bytes (q + 128) of `w`, selected by `sel`, to the exact
+// fp16 pair (q0, q1).  The perm builds the fp16 bit patterns 0x64uu = 1024 + u
+// for each byte u, so x - 1152 = q exactly.  dequant_pair: times the fp16
+// scale pair `s2`; one IEEE fp16 multiply of the exact operands gives
+// fp16_rne(q * s), the reference's half(float(q) * float(s))
+// (q8_gemm.metal:26) bit for bit.
+__device__ inline f16x2 q_pair(uint32_t w, uint32_t sel) {
   const f16x2 bias = {(f16)-1152.0f, (f16)-1152.0f};
-  return (x + bias) * s2;
+  return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, sel)) + bias;
+}
+__device__ inline f16x2 dequant_pair(uint32_t w, uint32_t sel, f16x2 s2) {
+  return q_pair(w, sel) * s2;
 }
 // byte selectors for v_perm_b32(0x64646464, w, sel): (b0,b1) and (b2,b3)
 constexpr uint32_t kSelLo = 0x04010400u;

@@ -200,15 +200,50 @@ __device__ inline void dma_group(desc_t wa, const Plan<MT> &p, uint32_t c, uint3
   dma16<I * 1024, I == 0>(wa, p.a_voff[I], c * 128, m0);
 }
 
+// Which of a chunk's prefetches (the A stage NA-1 chunks ahead, the weights WD
+// chunks ahead) are issued.  kSel: padded chunk counts; a prefetch past the
+// last chunk loads zeros through the empty descriptor (touching no memory),
+// chosen at run time.  kLive: every prefetch is live.  kLast0..kLast3: the
+// four chunks of the last trip of an unpadded loop, which issue only what is
+// live (kLast0 its A stage, the others nothing).  A load whose result is
+// never used must not be issued at all: the compiler sees the asm write its
+// registers at once and reuses them while the load is still in flight.
+enum Prefetch { kSel = 0, kLive = 1, kLast0 = 2, kLast1 = 3, kLast2 = 4, kLast3 = 5 };
+
+// The vmcnt counts of a chunk's two waits: `raw` at its start (chunk c+1's
+// weights, issued in chunk c+1-WD, have landed once only the loads issued
+// after them are outstanding) and `a` before its last k-step (chunk c+1's A
+// stage, issued in steps 0-1 of chunk c+2-NA).  The last trip issues fewer
+// loads, so fewer remain outstanding behind each target.
+template <int MT, int PF>
+struct Waits {
+  using G = Geometry<MT>;
+  static constexpr int raw = PF == kLast1 ? G::kPerChunk + MT
+                           : PF == kLast2 ? MT
+                           : PF == kLast3 ? 0
+                                          : G::kVmRaw;
+  static constexpr int a = PF == kLast0 ? G::LW + G::kPerChunk + MT
+                         : PF == kLast1 ? G::LW + MT
+                         : PF >= kLast2 ? 0
+                                        : G::kVmA;
+  static_assert(raw >= 0 && raw < 64 && a >= 0 && a < 64, "vmcnt range");
+};
+
 // The vector-memory issues of k-step s for chunk c's A stage (into `slot`) and
-// chunk cw's weights (into `w`); chunks past the last one load zeros (an empty
-// descriptor touches no memory).
-template <int MT>
+// chunk cw's weights (into `w`).
+template <int MT, int PF>
 __device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, uint32_t cw,
                                    const Plan<MT> &p, uint32_t lane) {
-  const desc_t wa = c < p.nchunks ? p.wa : p.zero;
-  const bool live = cw < p.nchunks;
-  const desc_t wq = live ? p.wq : p.zero, ws = live ? p.ws : p.zero;
+  static_assert(NA == 4 && WD == 4, "the last trip's issue plan assumes four stages");
+  if constexpr (PF >= kLast1) return;
+  desc_t wa = p.wa, wq = p.wq, ws = p.ws;
+  if constexpr (PF == kSel) {
+    wa = c < p.nchunks ? p.wa : p.zero;
+    const bool live = cw < p.nchunks;
+    wq = live ? p.wq : p.zero;
+    ws = live ? p.ws : p.zero;
+  }
+  constexpr bool W = PF != kLast0;  // weights issued
   const uint32_t m0 = lds_addr(slot) + p.a_lds;
   if (s == 0) {
     if constexpr (MT >= 2) dma_group<MT, 0>(wa, p, c, m0);
@@ -220,11 +255,13 @@ __device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, ui
       dma_group<MT, 2>(wa, p, c, m0);
       dma_group<MT, 3>(wa, p, c, m0);
     }
-    vload16(w.u[0][0], wq, lane * 16, p.w_soff[0] + cw * 2048);
+    if constexpr (W) vload16(w.u[0][0], wq, lane * 16, p.w_soff[0] + cw * 2048);
   } else if (s == 2) {
-    vload16<1024>(w.u[0][1], wq, lane * 16, p.w_soff[0] + cw * 2048);
-    vload16(w.u[1][0], wq, lane * 16, p.w_soff[1] + cw * 2048);
-  } else {
+    if constexpr (W) {
+      vload16<1024>(w.u[0][1], wq, lane * 16, p.w_soff[0] + cw * 2048);
+      vload16(w.u[1][0], wq, lane * 16, p.w_soff[1] + cw * 2048);
+    }
+  } else if constexpr (W) {
     vload16<1024>(w.u[1][1], wq, lane * 16, p.w_soff[1] + cw * 2048);
     vload2(w.s[0], ws, p.s_voff[0], cw * 128);
     vload2(w.s[1], ws, p.s_voff[1], cw * 128);
@@ -241,15 +278,19 @@ __device__ inline void load_a_frags(const uint8_t *As, int s, uint32_t h, uint32
     bf[i] = *reinterpret_cast<const f16x8 *>(As + (i * 32 + r) * 128 + phys);
 }
 
-// The k-step-s fragment of panel t: half (s & 1) of unit s >> 1.
+// The k-step-s fragment of panel t: half (s & 1) of unit s >> 1.  The four
+// pairs go through perm, subtract and multiply stage by stage (four
+// independent chains), so no packed op directly follows the one it depends on
+// (which would cost a wait state).
 __device__ inline f16x8 dequant_frag(const RawW &w, int t, int s) {
   const u32x4 u = w.u[t][s >> 1];
   const uint32_t b0 = (s & 1) ? u.z : u.x, b1 = (s & 1) ? u.w : u.y;
   const f16 sc = __builtin_bit_cast(f16, (uint16_t)w.s[t]);
   const f16x2 s2 = {sc, sc};
-  const f16x2 a0 = dequant_pair(b0, kSelLo, s2), a1 = dequant_pair(b0, kSelHi, s2);
-  const f16x2 a2 = dequant_pair(b1, kSelLo, s2), a3 = dequant_pair(b1, kSelHi, s2);
-  return (f16x8){a0.x, a0.y, a1.x, a1.y, a2.x, a2.y, a3.x, a3.y};
+  f16x2 a[4] = {q_pair(b0, kSelLo), q_pair(b0, kSelHi), q_pair(b1, kSelLo), q_pair(b1, kSelHi)};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = a[i] * s2;
+  return (f16x8){a[0].x, a[0].y, a[1].x, a[1].y, a[2].x, a[2].y, a[3].x, a[3].y};
 }
 
 // s_waitcnt lgkmcnt(0) with vmcnt and expcnt left at their maxima (gfx9
@@ -285,7 +326,7 @@ __device__ inline void schedule_step() {
 // activation fragments, and `nxt` receives chunk c+1's weights (loaded WD-1
 // chunks ago; waited for here).  `ld` (the same
 // register set as `cur`, free after step 0) receives chunk c+WD's weights.
-template <int MT>
+template <int MT, int PF>
 __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint32_t lane,
                              uint32_t h, uint32_t r, f32x16 (&acc)[2][MT], f16x8 (&w)[2][4],
                              f16x8 (&af)[MT], const RawW &cur, RawW &nxt, RawW &ld) {
@@ -293,13 +334,13 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint3
   const uint8_t *At = smem + (c % NA) * G::kStage;
   const uint8_t *An = smem + ((c + 1) % NA) * G::kStage;
   uint8_t *Af = smem + ((c + NA - 1) % NA) * G::kStage;
-  wait_weights<G::kVmRaw>(nxt);
+  wait_weights<Waits<MT, PF>::raw>(nxt);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     // the previous step's fragment reads (issued a whole step ago) have
     // landed: one wait here instead of one before each MFMA
     if (s == 3)
-      wait_then_barrier<G::kVmA>();  // chunk c+1's A stage is visible
+      wait_then_barrier<Waits<MT, PF>::a>();  // chunk c+1's A stage is visible
     __builtin_amdgcn_s_waitcnt(kLgkm0);
     f16x8 an[MT];
     if (s < 3)
@@ -317,7 +358,7 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint3
     for (int i = 0; i < MT; ++i)
       acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[1][s], af[i], acc[1][i], 0, 0, 0);
     w[1][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 1, (s + 3) & 3);
-    issue_loads<MT>(s, Af, c + NA - 1, ld, c + WD, p, lane);
+    issue_loads<MT, PF>(s, Af, c + NA - 1, ld, c + WD, p, lane);
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[i] = an[i];
     schedule_step<MT>();
@@ -325,7 +366,7 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint3
   }
 }
 
-template <int MT, int EPI>
+template <int MT, int EPI, bool PADDED>
 __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
                                                       const uint8_t *__restrict__ qs,
                                                       const f16 *__restrict__ sc,
@@ -411,7 +452,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
     uint8_t *slot = smem + (uint32_t)((j + NA - 1 + NA) % NA) * G::kStage;
     RawW &rw = j == -4 ? r0 : j == -3 ? r1 : j == -2 ? r2 : r3;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) issue_loads<MT>(st, slot, ca, rw, (uint32_t)(j + WD), p, lane);
+    for (int st = 0; st < 4; ++st) issue_loads<MT, kSel>(st, slot, ca, rw, (uint32_t)(j + WD), p, lane);
   }
   // chunk 0's weights and A stage, then its fragments
   wait_then_barrier<G::kVmPrologue>();
@@ -425,13 +466,33 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
 
   // ---- main loop: four chunks per trip (the weight register sets rotate).
   // The loop body stays one straight-line block: extra exits let the register
-  // allocator copy asm-loaded registers before their vmcnt wait.
-  const uint32_t cpad = (nchunks + WD - 1) / WD * WD;
-  for (uint32_t c = 0; c < cpad; c += 4) {
-    chunk<MT>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-    chunk<MT>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-    chunk<MT>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-    chunk<MT>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+  // allocator copy asm-loaded registers before their vmcnt wait.  Unpadded
+  // (the chunk count a multiple of four): every trip but the last prefetches
+  // only live chunks; the last trip is peeled, its prefetch targets known.
+  if constexpr (PADDED) {
+    const uint32_t cpad = (nchunks + WD - 1) / WD * WD;
+    for (uint32_t c = 0; c < cpad; c += 4) {
+      chunk<MT, kSel>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+      chunk<MT, kSel>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+      chunk<MT, kSel>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+      chunk<MT, kSel>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+    }
+  } else {
+    // at least two trips (the host checks): the loop is never skipped, so the
+    // prologue's registers reach the last trip only through it and need no
+    // copies on a path around it
+    uint32_t c = 0;
+    do {
+      chunk<MT, kLive>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+      chunk<MT, kLive>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+      chunk<MT, kLive>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+      chunk<MT, kLive>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+      c += 4;
+    } while (c + 2 * WD <= nchunks);
+    chunk<MT, kLast0>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+    chunk<MT, kLast1>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+    chunk<MT, kLast2>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+    chunk<MT, kLast3>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
   }
 
   // ---- epilogue.  Lane (h, r) holds D[n][m] for m = 32i + r and
@@ -564,8 +625,21 @@ int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const fl
     const int rc = workspace(part, T, &ws, &cnt);
     if (rc != MADI_OK) return rc;
   }
-  hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI>), dim3(T * splits), dim3(kWaves * 64), 0, stream(),
-                     A, qs, sc, C, bias, M, N, K, tiles_m, tiles_n, group_m, splits, ws, cnt);
+  // every split's chunk count a multiple of WD and at least 2*WD: the
+  // select-free loop
+  bool padded = false;
+  for (uint32_t s = 0; s < splits; ++s) {
+    const uint32_t n = (s + 1) * chunks / splits - s * chunks / splits;
+    if (n % WD || n < 2 * WD) padded = true;
+  }
+  if (padded)
+    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, true>), dim3(T * splits), dim3(kWaves * 64), 0,
+                       stream(), A, qs, sc, C, bias, M, N, K, tiles_m, tiles_n, group_m, splits,
+                       ws, cnt);
+  else
+    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false>), dim3(T * splits), dim3(kWaves * 64), 0,
+                       stream(), A, qs, sc, C, bias, M, N, K, tiles_m, tiles_n, group_m, splits,
+                       ws, cnt);
   return check_launch("madi_q8_gemm");
 }
 

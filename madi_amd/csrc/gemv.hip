@@ -87,13 +87,6 @@ __device__ inline void load_chunk(ChunkW &b, rsrc_t wq, rsrc_t ws, uint32_t K, u
   b.s = __builtin_amdgcn_raw_buffer_load_b16(ws, s_voff, (uint32_t)panel_chunk_sc(K, p, R, c) * 2, 0);
 }
 
-// The exact fp16 pair (q0, q1) of two biased bytes of `w` selected by `sel`:
-// v_perm_b32 builds (1024 + u0, 1024 + u1), a packed subtract removes 1152.
-__device__ inline f16x2 q_pair(uint32_t w, uint32_t sel) {
-  const f16x2 bias = {(f16)-1152.0f, (f16)-1152.0f};
-  return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, sel)) + bias;
-}
-
 // sum_i x[i] * q[i] over one 16-byte unit, fp16 activations: v_dot2_f32_f16
 // multiplies two exact fp16 pairs (exact products) and adds them in fp32.
 __device__ inline float unit_dot(const u32x4 &w, const f16 *x16, float part) {
