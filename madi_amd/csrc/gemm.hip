@@ -65,7 +65,8 @@ namespace {
 
 constexpr int kPanelsPerTile = 8;
 constexpr int kWaves = 4;  // one wave per SIMD
-constexpr int NA = 4;      // activation ring stages
+constexpr int NA = 8;      // activation ring stages
+constexpr int DA = 4;      // A stages are copied DA chunks ahead of use
 constexpr int WD = 4;      // weight register sets (chunks of weight prefetch)
 constexpr int kCStride = kPanelsPerTile * kPanelRows * 2 + 16;  // epilogue tile row pitch
 
@@ -87,13 +88,16 @@ struct Geometry {
   // chunk c+1-WD) have landed once only the loads of the WD-2 chunks after
   // them are outstanding
   static constexpr int kVmRaw = (WD - 2) * kPerChunk;
-  // before step 3 of chunk c: chunk c+1's A stage (issued in steps 0-1 of
-  // chunk c+2-NA, followed by 6 weight loads) has landed
-  static constexpr int kVmA = LW + (NA - 3) * kPerChunk + kBeforeStep3;
-  // prologue: virtual chunks -WD..-1 issue the same pattern; chunk 0's A stage
-  // (virtual chunk 1-NA) and weights (virtual chunk -WD) have landed
-  static constexpr int kVmPrologue = LW + (NA - 2) * kPerChunk;
-  static_assert(kVmRaw < 64 && kVmA < 64, "vmcnt range");
+  // before step 3 of an odd chunk c, whose barrier publishes the A stages of
+  // chunks c+1 and c+2: chunk c+2's stage (issued in steps 0-1 of chunk
+  // c+2-DA, followed by that chunk's 6 weight loads, chunk c-1's loads and
+  // chunk c's first three steps) has landed
+  static constexpr int kVmA = LW + (DA - 3) * kPerChunk + kBeforeStep3;
+  // prologue: virtual chunks -DA..-1 issue the same pattern; chunk 0's weights
+  // (virtual chunk -WD) and the A stages of chunks 0 and 1 (virtual chunks -DA
+  // and 1-DA) have landed
+  static constexpr int kVmPrologue = LW + (DA - 2) * kPerChunk;
+  static_assert(kVmRaw < 64 && kVmA < 64 && kVmPrologue < 64, "vmcnt range");
 };
 
 typedef __attribute__((address_space(3))) uint8_t lds_u8;
@@ -182,6 +186,22 @@ __device__ inline void wait_weights(RawW &w) {
                : [n] "n"(N));
 }
 
+// After the K loop: wait for every outstanding load, with the four weight
+// register sets as operands of the wait.  The last prefetches' registers are
+// dead to the compiler once the loop ends, and it would otherwise reuse them
+// (for the epilogue's accumulator reads) while loads into them are still in
+// flight.
+__device__ inline void drain(RawW &a, RawW &b, RawW &c, RawW &d) {
+  asm volatile("s_waitcnt vmcnt(0)"
+               : "+v"(a.u[0][0]), "+v"(a.u[0][1]), "+v"(a.u[1][0]), "+v"(a.u[1][1]), "+v"(a.s[0]),
+                 "+v"(a.s[1]), "+v"(b.u[0][0]), "+v"(b.u[0][1]), "+v"(b.u[1][0]), "+v"(b.u[1][1]),
+                 "+v"(b.s[0]), "+v"(b.s[1])::"memory");
+  asm volatile("s_waitcnt vmcnt(0)"
+               : "+v"(c.u[0][0]), "+v"(c.u[0][1]), "+v"(c.u[1][0]), "+v"(c.u[1][1]), "+v"(c.s[0]),
+                 "+v"(c.s[1]), "+v"(d.u[0][0]), "+v"(d.u[0][1]), "+v"(d.u[1][0]), "+v"(d.u[1][1]),
+                 "+v"(d.s[0]), "+v"(d.s[1])::"memory");
+}
+
 // Per-wave load plan, fixed for the whole K loop.
 template <int MT>
 struct Plan {
@@ -200,14 +220,14 @@ __device__ inline void dma_group(desc_t wa, const Plan<MT> &p, uint32_t c, uint3
   dma16<I * 1024, I == 0>(wa, p.a_voff[I], c * 128, m0);
 }
 
-// Which of a chunk's prefetches (the A stage NA-1 chunks ahead, the weights WD
+// Which of a chunk's prefetches (the A stage DA chunks ahead, the weights WD
 // chunks ahead) are issued.  kSel: padded chunk counts; a prefetch past the
 // last chunk loads zeros through the empty descriptor (touching no memory),
 // chosen at run time.  kLive: every prefetch is live.  kLast0..kLast3: the
-// four chunks of the last trip of an unpadded loop, which issue only what is
-// live (kLast0 its A stage, the others nothing).  A load whose result is
-// never used must not be issued at all: the compiler sees the asm write its
-// registers at once and reuses them while the load is still in flight.
+// four chunks of the last trip of an unpadded loop, all of whose prefetches
+// lie past the end: they issue nothing.  A load whose result is never used
+// must not be issued at all: the compiler sees the asm write its registers at
+// once and reuses them while the load is still in flight.
 enum Prefetch { kSel = 0, kLive = 1, kLast0 = 2, kLast1 = 3, kLast2 = 4, kLast3 = 5 };
 
 // The vmcnt counts of a chunk's two waits: `raw` at its start (chunk c+1's
@@ -218,14 +238,10 @@ enum Prefetch { kSel = 0, kLive = 1, kLast0 = 2, kLast1 = 3, kLast2 = 4, kLast3 
 template <int MT, int PF>
 struct Waits {
   using G = Geometry<MT>;
-  static constexpr int raw = PF == kLast1 ? G::kPerChunk + MT
-                           : PF == kLast2 ? MT
-                           : PF == kLast3 ? 0
+  static constexpr int raw = PF == kLast1 ? G::kPerChunk
+                           : PF >= kLast2 ? 0
                                           : G::kVmRaw;
-  static constexpr int a = PF == kLast0 ? G::LW + G::kPerChunk + MT
-                         : PF == kLast1 ? G::LW + MT
-                         : PF >= kLast2 ? 0
-                                        : G::kVmA;
+  static constexpr int a = PF == kLast1 ? G::LW : PF == kLast3 ? 0 : G::kVmA;
   static_assert(raw >= 0 && raw < 64 && a >= 0 && a < 64, "vmcnt range");
 };
 
@@ -234,8 +250,8 @@ struct Waits {
 template <int MT, int PF>
 __device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, uint32_t cw,
                                    const Plan<MT> &p, uint32_t lane) {
-  static_assert(NA == 4 && WD == 4, "the last trip's issue plan assumes four stages");
-  if constexpr (PF >= kLast1) return;
+  static_assert(DA == 4 && WD == 4, "the last trip's issue plan assumes four-chunk prefetch");
+  if constexpr (PF >= kLast0) return;
   desc_t wa = p.wa, wq = p.wq, ws = p.ws;
   if constexpr (PF == kSel) {
     wa = c < p.nchunks ? p.wa : p.zero;
@@ -243,7 +259,7 @@ __device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, ui
     wq = live ? p.wq : p.zero;
     ws = live ? p.ws : p.zero;
   }
-  constexpr bool W = PF != kLast0;  // weights issued
+  constexpr bool W = true;
   const uint32_t m0 = lds_addr(slot) + p.a_lds;
   if (s == 0) {
     if constexpr (MT >= 2) dma_group<MT, 0>(wa, p, c, m0);
@@ -326,21 +342,23 @@ __device__ inline void schedule_step() {
 // activation fragments, and `nxt` receives chunk c+1's weights (loaded WD-1
 // chunks ago; waited for here).  `ld` (the same
 // register set as `cur`, free after step 0) receives chunk c+WD's weights.
-template <int MT, int PF>
+template <int MT, int PF, bool ODD>
 __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint32_t lane,
                              uint32_t h, uint32_t r, f32x16 (&acc)[2][MT], f16x8 (&w)[2][4],
                              f16x8 (&af)[MT], const RawW &cur, RawW &nxt, RawW &ld) {
   using G = Geometry<MT>;
   const uint8_t *At = smem + (c % NA) * G::kStage;
   const uint8_t *An = smem + ((c + 1) % NA) * G::kStage;
-  uint8_t *Af = smem + ((c + NA - 1) % NA) * G::kStage;
+  uint8_t *Af = smem + ((c + DA) % NA) * G::kStage;
   wait_weights<Waits<MT, PF>::raw>(nxt);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     // the previous step's fragment reads (issued a whole step ago) have
     // landed: one wait here instead of one before each MFMA
-    if (s == 3)
-      wait_then_barrier<Waits<MT, PF>::a>();  // chunk c+1's A stage is visible
+    // odd chunks: the A stages of chunks c+1 and c+2 become visible, and the
+    // stages of chunks c-1 and c retire (refilled from chunk c+DA-2 on); an
+    // even chunk reads chunk c+1's stage, published one chunk earlier
+    if (s == 3 && ODD) wait_then_barrier<Waits<MT, PF>::a>();
     __builtin_amdgcn_s_waitcnt(kLgkm0);
     f16x8 an[MT];
     if (s < 3)
@@ -358,7 +376,7 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint3
     for (int i = 0; i < MT; ++i)
       acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[1][s], af[i], acc[1][i], 0, 0, 0);
     w[1][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 1, (s + 3) & 3);
-    issue_loads<MT, PF>(s, Af, c + NA - 1, ld, c + WD, p, lane);
+    issue_loads<MT, PF>(s, Af, c + DA, ld, c + WD, p, lane);
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[i] = an[i];
     schedule_step<MT>();
@@ -439,22 +457,23 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
     for (int i = 0; i < MT; ++i) acc[t][i] = (f32x16){};
 
   // ---- prologue: the loads the steady state would have issued before chunk 0
-  // (virtual chunks -WD .. -1), in the same order, so the loop's vmcnt waits
-  // hold from the first chunk on.  Virtual chunk j loads A stage j+NA-1 (a
-  // negative, i.e. wrapped and out-of-range, stage loads zeros into a slot
-  // nothing reads) and weights j+WD; register set k receives chunks k, k+WD, ...
+  // (virtual chunks -4 .. -1), in the same order, so the loop's vmcnt waits
+  // hold from the first chunk on.  Virtual chunk j loads A stage j+DA and
+  // weights j+WD (stages and weights past the last chunk load zeros); register
+  // set k receives chunks k, k+WD, ...
   RawW r0, r1, r2, r3;
-  static_assert(WD == 4, "the loop below rotates four weight register sets");
-  static_assert(NA >= 3 && NA <= WD + 1, "the prologue covers the first NA-1 stages");
+  static_assert(WD == 4 && DA == 4, "the loop below rotates four weight register sets");
+  static_assert(NA >= DA + 2, "an A stage is refilled only after the barrier that retires it");
 #pragma unroll
-  for (int j = -WD; j < 0; ++j) {
-    const uint32_t ca = (uint32_t)(j + NA - 1);
-    uint8_t *slot = smem + (uint32_t)((j + NA - 1 + NA) % NA) * G::kStage;
+  for (int j = -4; j < 0; ++j) {
+    uint8_t *slot = smem + (uint32_t)(j + DA) * G::kStage;
     RawW &rw = j == -4 ? r0 : j == -3 ? r1 : j == -2 ? r2 : r3;
 #pragma unroll
-    for (int st = 0; st < 4; ++st) issue_loads<MT, kSel>(st, slot, ca, rw, (uint32_t)(j + WD), p, lane);
+    for (int st = 0; st < 4; ++st)
+      issue_loads<MT, kSel>(st, slot, (uint32_t)(j + DA), rw, (uint32_t)(j + WD), p, lane);
   }
-  // chunk 0's weights and A stage, then its fragments
+  // chunk 0's weights and the A stages of chunks 0 and 1 (chunk 0 reads
+  // chunk 1's stage without a barrier of its own), then chunk 0's fragments
   wait_then_barrier<G::kVmPrologue>();
   wait_weights<G::kVmPrologue>(r0);
   f16x8 w[2][4], af[MT];
@@ -472,10 +491,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   if constexpr (PADDED) {
     const uint32_t cpad = (nchunks + WD - 1) / WD * WD;
     for (uint32_t c = 0; c < cpad; c += 4) {
-      chunk<MT, kSel>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-      chunk<MT, kSel>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-      chunk<MT, kSel>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-      chunk<MT, kSel>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+      chunk<MT, kSel, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+      chunk<MT, kSel, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+      chunk<MT, kSel, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+      chunk<MT, kSel, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
     }
   } else {
     // at least two trips (the host checks): the loop is never skipped, so the
@@ -483,17 +502,19 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
     // copies on a path around it
     uint32_t c = 0;
     do {
-      chunk<MT, kLive>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-      chunk<MT, kLive>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-      chunk<MT, kLive>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-      chunk<MT, kLive>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+      chunk<MT, kLive, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+      chunk<MT, kLive, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+      chunk<MT, kLive, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+      chunk<MT, kLive, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
       c += 4;
     } while (c + 2 * WD <= nchunks);
-    chunk<MT, kLast0>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-    chunk<MT, kLast1>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-    chunk<MT, kLast2>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-    chunk<MT, kLast3>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+    chunk<MT, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+    chunk<MT, kLast1, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+    chunk<MT, kLast2, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+    chunk<MT, kLast3, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
   }
+
+  drain(r0, r1, r2, r3);
 
   // ---- epilogue.  Lane (h, r) holds D[n][m] for m = 32i + r and
   // n = 32(2w + t) + 8g + 4h + e (acc[t][i][4g + e]).  Every wave must finish
