@@ -158,13 +158,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   if (i1 < pieces) xv1 = __builtin_amdgcn_raw_buffer_load_b128(xr, i1 * 16, 0, 0);
 
   const rsrc_t wq = make_rsrc(a.qs, a.n * K), ws = make_rsrc(a.sc, a.n * (K / 32) * 2);
+  // chunks past the wave's range load through an empty resource: no memory
+  // access, zeros returned, so their scale is 0 and they add exactly nothing.
+  // Every window load is then unconditional, which keeps each window slot in
+  // the same registers from trip to trip (a conditional load makes the
+  // compiler copy the slot at the loop back edge, and a copy must first wait
+  // for the load that was just issued, collapsing the window).
+  const rsrc_t wz = make_rsrc(a.qs, 0);
   const uint32_t rr = live ? r : R - 1;
   const uint32_t w_voff = (h * R + rr) * 16, s_voff = (h * R + rr) * 2;
   // the first kWin chunks of this wave's range go in flight behind x
   ChunkW win[kWin];
 #pragma unroll
-  for (int k = 0; k < kWin; ++k)
-    if (c0 + k < c1) load_chunk(win[k], wq, ws, K, c0 + k, p, R, w_voff, s_voff);
+  for (int k = 0; k < kWin; ++k) {
+    const bool in = c0 + k < c1;
+    load_chunk(win[k], in ? wq : wz, in ? ws : wz, K, c0 + k, p, R, w_voff, s_voff);
+  }
 
   // stage x
   for (uint32_t i = threadIdx.x; i < pieces; i += 256) {
@@ -181,10 +190,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   for (uint32_t c = c0; c < c1; c += kWin) {
 #pragma unroll
     for (int k = 0; k < kWin; ++k) {
-      if (c + k < c1) {
-        accumulate<XT>(win[k], c + k, xs, h, acc);
-        if (c + k + kWin < c1) load_chunk(win[k], wq, ws, K, c + k + kWin, p, R, w_voff, s_voff);
-      }
+      // a chunk past the range (zeros, scale 0) reads the x of the range's
+      // last chunk, so its partial stays finite and 0 * partial is exact
+      const uint32_t cc = c + k < c1 ? c + k : c1 - 1;
+      accumulate<XT>(win[k], cc, xs, h, acc);
+      const uint32_t cn = c + k + kWin;
+      const bool in = cn < c1;
+      load_chunk(win[k], in ? wq : wz, in ? ws : wz, K, cn, p, R, w_voff, s_voff);
+      // keep the next slot's math behind this reload: interleaved, both
+      // slots would have to land before either is reissued
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
