@@ -140,10 +140,27 @@ def test_gemm_parity_small(q, m, n, k):
     assert tight_ok(c, a, qs, sc)
 
 
+@pytest.mark.parametrize("k", [128, 256, 320, 512, 768, 1024])
+@pytest.mark.parametrize("m", [20, 33, 130])
+def test_gemm_k_loop_shapes(q, m, k):
+    """Every K-loop shape at each m-tile height (32, 64, 128 rows): chunk counts
+    below eight or not a multiple of four run the padded loop (2, 4, 5
+    chunks); 8 chunks is one full trip plus the peeled last trip, 12 and 16
+    two and three trips."""
+    n = 320
+    say(f"gemm k-loop m={m} n={n} k={k}")
+    a, qs, sc = synth.gemm_case(m * 13 + k, m, n, k)
+    c = _gemm(q, a, qs, sc)
+    ref = O.q8_gemm_rows(a, qs, sc, threads=8)
+    assert normwise(c, ref) <= TOL, normwise(c, ref)
+    assert tight_ok(c, a, qs, sc)
+
+
 @pytest.mark.parametrize("m,n,k", [
     (257, 1280, 5120),  # 15 tiles x 4 K splits of 20 chunks, M tail
     (20, 512, 4096),    # 32-row tiles, 2 tiles x 4 splits of 16 chunks
     (64, 768, 6144),    # 64-row tiles, 3 tiles x 4 splits of 24 chunks
+    (130, 512, 4288),   # 67 chunks: 4 splits of 16-17 chunks (padded loop)
 ])
 def test_gemm_split_k(q, m, n, k):
     """Long K over few tiles: the workgroups of a tile split K and the last
