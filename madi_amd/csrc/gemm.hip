@@ -594,7 +594,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
           v[3] += b4[g].w;
           if constexpr (EPI == MADI_EPI_BIAS_GELU) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = gelu_erf(v[e]);
+            for (int e = 0; e < 4; ++e) v[e] = gelu_erf_fast(v[e]);
           }
         }
         const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};

@@ -60,6 +60,33 @@ def tight_ok(c, a, qs, sc):
     return bool(np.all(np.abs(c.astype(np.float64) - exact) <= bound * 1.001))
 
 
+def gelu_as64(v):
+    """The erf-form GELU with the Abramowitz & Stegun 7.1.26 erf
+    (graph_helpers.metal:460-473), evaluated in float64."""
+    z = v / np.sqrt(2.0)
+    az = np.abs(z)
+    t = 1.0 / (1.0 + 0.3275911 * az)
+    poly = t * (0.254829592 + t * (-0.284496736 + t * (1.421413741 + t * (-1.453152027
+                                                                           + t * 1.061405429))))
+    erf = np.sign(z) * (1.0 - poly * np.exp(-az * az))
+    return 0.5 * v * (1.0 + erf)
+
+
+def tight_epi_ok(c, a, qs, sc, bias, gelu):
+    """Element-wise for the bias / bias+GELU epilogues: the kernel must equal
+    epi(sum_k a_k * fp16_rne(q_k s_k) + bias) up to fp32 accumulation (scaled
+    by GELU's largest slope, 1.13), the GELU formula's fp32 evaluation (a few
+    ulps) and one f16 output rounding."""
+    w16 = O.dequant_q8_f16(qs, sc).astype(np.float64).T  # [N][K]
+    a64 = a.astype(np.float64)
+    v = a64 @ w16.T + bias.astype(np.float64)[None, :]
+    acc = a.shape[1] * 2.0**-24 * (np.abs(a64) @ np.abs(w16).T) + 2.0**-24 * np.abs(v)
+    exact, slope = (gelu_as64(v), 1.13) if gelu else (v, 1.0)
+    bound = (2.0**-11 * np.abs(exact) + slope * acc + (4e-7 * (1.0 + np.abs(v)) if gelu else 0)
+             + 2.0**-25)
+    return bool(np.all(np.abs(c.astype(np.float64) - exact) <= bound * 1.001))
+
+
 def normwise(c, ref):
     c = c.astype(np.float64)
     ref = ref.astype(np.float64)
@@ -197,6 +224,7 @@ def test_gemm_bias_epilogues(q, gelu):
     ref = O.q8_gemm_rows(a, qs, sc, bias=bias,
                          epilogue=O.EPI_BIAS_GELU if gelu else O.EPI_BIAS, threads=8)
     assert normwise(c, ref) <= TOL
+    assert tight_epi_ok(c, a, qs, sc, bias, gelu)
 
 
 @pytest.mark.parametrize("name,n,k", [("fc1", 5120, 1280), ("fc2", 1280, 5120), ("qkv", 3840, 1280)])
