@@ -69,6 +69,7 @@ constexpr int NA = 8;      // activation ring stages
 constexpr int DA = 4;      // A stages are copied DA chunks ahead of use
 constexpr int WD = 4;      // weight register sets (chunks of weight prefetch)
 constexpr int kCStride = kPanelsPerTile * kPanelRows * 2 + 16;  // epilogue tile row pitch
+constexpr uint32_t kMaxSplits = 4;  // split-K workgroups per tile
 
 template <int MT>
 struct Geometry {
@@ -548,23 +549,54 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
       arrived = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
     if (arrived != splits - 1) return;
-    for (uint32_t s2 = 0; s2 < splits; ++s2) {
-      if (s2 == split) continue;
+    // Sum the splits' partials in split order, this workgroup's own from its
+    // registers at its own position, so the result does not depend on which
+    // workgroup arrives last.  One fully unrolled pass over the register
+    // groups, each group's loads for every split issued together, keeps many
+    // loads in flight (a pass per split waited out the memory latency once
+    // per split).
+    static_assert(kMaxSplits == 4, "the reduction below unrolls four splits");
+    // every load is issued (a split past `splits`, or this workgroup's own,
+    // reads zeros through an empty resource), and the own partial enters by a
+    // 0/1 factor: no branches, so the loads of many groups stay in flight
+    __amdgpu_buffer_rsrc_t rs[kMaxSplits];
+    float mine[kMaxSplits];
+    const __amdgpu_buffer_rsrc_t zr = __builtin_amdgcn_make_buffer_rsrc(ws, 0, 0, 0x00020000);
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+    for (uint32_t s2 = 0; s2 < kMaxSplits; ++s2) {
+      rs[s2] = s2 < splits && s2 != split ? wsr : zr;
+      mine[s2] = s2 == split ? 1.0f : 0.0f;
+    }
+    // register groups q = (t, i, g) in order; group q + kAhead's loads are
+    // issued before group q is summed, so the waits only cover old loads
+    constexpr int kGroups = 2 * MT * 4, kAhead = 6;
+    auto load_group = [&](int q, f32x4 (&dst)[kMaxSplits]) {
+      const uint32_t voff = ((wave * kGroups + q) * 64 + lane) * 16;
 #pragma unroll
-        for (int i = 0; i < MT; ++i)
+      for (uint32_t s2 = 0; s2 < kMaxSplits; ++s2)
+        dst[s2] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                rs[s2], voff, (tile * splits + s2) * kPart, kSc1));
+    };
+    f32x4 ring[kAhead + 1][kMaxSplits];
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const f32x4 v = __builtin_bit_cast(
-                f32x4, __builtin_amdgcn_raw_buffer_load_b128(
-                           wsr, ((((wave * 2 + t) * MT + i) * 4 + g) * 64 + lane) * 16,
-                           (tile * splits + s2) * kPart, kSc1));
-            acc[t][i][4 * g] += v.x;
-            acc[t][i][4 * g + 1] += v.y;
-            acc[t][i][4 * g + 2] += v.z;
-            acc[t][i][4 * g + 3] += v.w;
-          }
+    for (int q = 0; q < kAhead; ++q) load_group(q, ring[q]);
+#pragma unroll
+    for (int q = 0; q < kGroups; ++q) {
+      if (q + kAhead < kGroups) load_group(q + kAhead, ring[(q + kAhead) % (kAhead + 1)]);
+      const int t = q / (MT * 4), i = (q / 4) % MT, g = q % 4;
+      const f32x4 own = {acc[t][i][4 * g], acc[t][i][4 * g + 1], acc[t][i][4 * g + 2],
+                         acc[t][i][4 * g + 3]};
+      f32x4 part[kMaxSplits];
+#pragma unroll
+      for (uint32_t s2 = 0; s2 < kMaxSplits; ++s2)
+        part[s2] = ring[q % (kAhead + 1)][s2] + own * mine[s2];
+      // splits past `splits` add exact zeros
+      const f32x4 sum = ((part[0] + part[1]) + part[2]) + part[3];
+      acc[t][i][4 * g] = sum.x;
+      acc[t][i][4 * g + 1] = sum.y;
+      acc[t][i][4 * g + 2] = sum.z;
+      acc[t][i][4 * g + 3] = sum.w;
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (threadIdx.x == 0)  // ready for the next launch
       __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
@@ -621,6 +653,22 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   }
 }
 
+// Too few tiles to fill the GPU and a long K (fc2 at M = 1500 with 64-row
+// tiles: 120 tiles, 80 chunks): split K over up to four workgroups per tile,
+// >= 16 chunks each.  The partial sums travel through memory (about 1 us per
+// MB of partials), which only pays off when each split keeps a long K range.
+uint32_t split_count(uint32_t tiles, uint32_t chunks) {
+  if (tiles >= 160 || chunks < 64) return 1;
+  uint32_t splits = 240 / tiles;
+  if (splits > kMaxSplits) splits = kMaxSplits;
+  if (splits > chunks / 16) splits = chunks / 16;
+  return splits < 1 ? 1 : splits;
+}
+
+uint32_t tile_count(uint32_t M, uint32_t N, uint32_t MT) {
+  return (M + 32 * MT - 1) / (32 * MT) * ((N + 255) / 256);
+}
+
 template <int MT, int EPI>
 int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const float *bias,
                 uint32_t M, uint32_t N, uint32_t K) {
@@ -628,17 +676,7 @@ int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const fl
   const uint32_t tiles_n = (N + 255) / 256;
   const uint32_t group_m = tiles_m < 6 ? tiles_m : 6;
   const uint32_t T = tiles_m * tiles_n, chunks = K / kChunkK;
-  // Too few tiles to fill the GPU and a long K (fc2 at M = 1500: 60 tiles, 80
-  // chunks): split K over up to four workgroups per tile, >= 16 chunks each.
-  // The partial sums travel through memory (about 1 us per MB of partials),
-  // which only pays off when each split keeps a long K range.
-  uint32_t splits = 1;
-  if (T < 160 && chunks >= 64) {
-    splits = 240 / T;
-    if (splits > 4) splits = 4;
-    if (splits > chunks / 16) splits = chunks / 16;
-    if (splits < 1) splits = 1;
-  }
+  const uint32_t splits = split_count(T, chunks);
   float *ws = nullptr;
   uint32_t *cnt = nullptr;
   if (splits > 1) {
@@ -700,6 +738,10 @@ extern "C" int madi_q8_gemm(const void *a, const void *qs, const void *scales, v
   const f16 *S = static_cast<const f16 *>(scales);
   f16 *C = static_cast<f16 *>(c);
   if (m <= 32) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k);
-  if (m <= 64) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k);
+  // 128-row tiles, unless they would split K: then 64-row tiles, which halve
+  // the split count and the partial sums through memory (fc2 at M = 1500:
+  // 2 splits of 40 chunks instead of 4 of 20, 35 -> 30.5 us)
+  if (m <= 64 || split_count(tile_count(m, n, 4), k / kChunkK) > 1)
+    return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k);
   return dispatch_epi<4>(epilogue, A, Q, S, C, bias, m, n, k);
 }

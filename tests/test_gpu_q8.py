@@ -184,10 +184,12 @@ def test_gemm_k_loop_shapes(q, m, k):
 
 
 @pytest.mark.parametrize("m,n,k", [
-    (257, 1280, 5120),  # 15 tiles x 4 K splits of 20 chunks, M tail
+    (257, 1280, 5120),  # 64-row tiles: 25 tiles x 4 K splits of 20 chunks, M tail
     (20, 512, 4096),    # 32-row tiles, 2 tiles x 4 splits of 16 chunks
     (64, 768, 6144),    # 64-row tiles, 3 tiles x 4 splits of 24 chunks
     (130, 512, 4288),   # 67 chunks: 4 splits of 16-17 chunks (padded loop)
+    (1000, 1280, 5120),  # 80 tiles x 3 splits of 26-27 chunks (padded loop)
+    (1100, 1280, 5120),  # 90 tiles x 2 splits of 40 chunks
 ])
 def test_gemm_split_k(q, m, n, k):
     """Long K over few tiles: the workgroups of a tile split K and the last
