@@ -129,23 +129,31 @@ __device__ inline void accumulate(const ChunkW &b, uint32_t c, const XT *xs, uin
 }
 
 template <typename XT, int MODE>
+//
+// Grid (x, y) = (panel, K split).  The arguments are scalars in the order the
+// kernel first needs them, so the leading ones arrive preloaded in SGPRs, and
+// the set-up has no integer division: split s covers chunks [s * cper +
+// min(s, crem), + cper + (s < crem)).
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q8_gemv_kernel(
-    GemvArgs a) {
+    const uint8_t *qs, const f16 *sc, const void *x, uint32_t n, uint32_t k, uint32_t cper,
+    uint32_t crem, float *out, const float *bias, float *wsp, uint32_t *cnt, const float *qb,
+    const float *vb, float *kc, float *vc, const uint32_t *pos) {
+  const GemvArgs a{out, x, qs, sc, bias, n, k, qb, vb, kc, vc, pos, gridDim.y, wsp, cnt};
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const uint32_t K = a.k, C = K / kChunkK;
+  const uint32_t K = a.k;
   XT *xs = reinterpret_cast<XT *>(smem);                        // [K]
   float *red = reinterpret_cast<float *>(smem + lds_bytes<XT>(K) - kWaves * 32 * 4);  // [4][32]
 
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
-  const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
-  const uint32_t p = blockIdx.x % np, split = blockIdx.x / np;
+  const uint32_t p = blockIdx.x, split = blockIdx.y;
   const uint32_t R = panel_rows(a.n, p);
   const bool live = r < R;
-  // this workgroup's K chunks [cs, ce), split four ways over the waves
-  const uint32_t cs = split * C / a.splits, ce = (split + 1) * C / a.splits;
-  const uint32_t c0 = cs + (wave * (ce - cs)) / kWaves, c1 = cs + ((wave + 1) * (ce - cs)) / kWaves;
+  // this workgroup's K chunks [cs, cs + nck), split four ways over the waves
+  const uint32_t cs = split * cper + (split < crem ? split : crem);
+  const uint32_t nck = cper + (split < crem ? 1 : 0);
+  const uint32_t c0 = cs + (wave * nck) / kWaves, c1 = cs + ((wave + 1) * nck) / kWaves;
 
   // ---- x: load first (16 bytes per thread and piece), then the weights.
   // Lanes past a partial panel's last row read row R-1 (in bounds; their sums
@@ -274,7 +282,9 @@ int launch(const char *what, const GemvArgs &a) {
     if (int rc = workspace((size_t)np * b.splits * 32 * 4, np, &b.ws, &b.cnt)) return rc;
   }
   const size_t lds = lds_bytes<XT>(a.k);
-  hipLaunchKernelGGL((q8_gemv_kernel<XT, MODE>), dim3(np * b.splits), dim3(256), lds, stream(), b);
+  hipLaunchKernelGGL((q8_gemv_kernel<XT, MODE>), dim3(np, b.splits), dim3(256), lds, stream(),
+                     b.qs, b.sc, b.x, b.n, b.k, C / b.splits, C % b.splits, b.out, b.bias, b.ws,
+                     b.cnt, b.qb, b.vb, b.kc, b.vc, b.pos);
   return check_launch(what);
 }
 

@@ -13,27 +13,29 @@
 // the result away from the fp32 reference of test_batchproj.zig:72-78).
 //
 // Workgroup: P weight panels (32 rows each; P = 4 for the 51866-row vocab
-// matrix, 1 otherwise) x one slice of 32 activation rows, KW waves splitting
-// K (8 for single panels, 4 for panel groups).  Per 64-wide K chunk a wave
-// loads each panel's two 16-byte units per lane (lane (h, r): row r's 32
-// weights of quantisation block h) and scale, and the slice's 32 x 64 f32
-// activations with coalesced loads (each instruction: four whole 256-byte row
-// segments), rounds them to f16 into its own LDS tile and reads them back as
-// MFMA fragments (lane (h, c): row c, the same 32 k).  Four
+// matrix, 1 otherwise) x one slice of 32 activation rows (the MFMA columns),
+// KW waves splitting K.  Per 64-wide K chunk a wave loads each panel's two
+// 16-byte units per lane (lane (h, r): row r's 32 weights of quantisation
+// block h) and scale, and the slice's first XR rows (8, 16 or 32: the rows a
+// batch of M <= XR has) of 64 f32 activations with coalesced loads (each
+// instruction: four whole 256-byte row segments), rounds them to f16 into its
+// own LDS tile and reads them back as MFMA fragments (lane (h, c): row c, the
+// same 32 k; columns c >= XR are zeros without a load).  Four
 // v_mfma_f32_32x32x16_f16 per panel and chunk, with the weight as the A operand
 // (rows n) and the activations as B (columns m); K order of step s: k = 32h +
 // 8s + e for both operands, as in the GEMM.  Activation rows past M load as
-// zeros (outside the buffer resource), so small M costs no extra memory
-// traffic.  Each wave keeps a two-chunk window in flight; the K partial tiles
-// meet in LDS and four waves store one quarter each.
+// zeros (outside the buffer resource).  The projections of a decode step are
+// small (1.6 - 6.5 MB of weights), so their time is load latency: each wave
+// keeps WIN chunks in flight, enough that the K range of most waves is one
+// round of loads; the K partial tiles meet in LDS and four waves store one
+// quarter each.
 #include "common.h"
 
 using namespace madi;
 
 namespace {
 
-constexpr int kWin = 2;     // chunks in flight per wave
-constexpr uint32_t kSlice = 32;  // activation rows per workgroup
+constexpr uint32_t kSlice = 32;  // activation rows per workgroup (MFMA columns)
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ inline rsrc_t make_rsrc(const void *base, uint32_t bytes) {
@@ -51,18 +53,18 @@ struct Plan {
 };
 
 // One chunk's loads for a lane: two weight units and the block scale per
-// panel, and 8 x 16 bytes of activations in a coalesced pattern: piece i is
-// row 4i + lane/16, floats 4 * (lane % 16) .. +3 of the chunk (each load
+// panel, and XR/4 x 16 bytes of activations in a coalesced pattern: piece i
+// is row 4i + lane/16, floats 4 * (lane % 16) .. +3 of the chunk (each load
 // instruction reads four whole 256-byte row segments).
-template <int P>
+template <int P, int XR>
 struct Chunk {
   u32x4 w[P][2];
   uint32_t s[P];
-  f32x4 x[8];
+  f32x4 x[XR / 4];
 };
 
-template <int P>
-__device__ inline void load_chunk(Chunk<P> &b, const Plan<P> &pl, uint32_t c) {
+template <int P, int XR>
+__device__ inline void load_chunk(Chunk<P, XR> &b, const Plan<P> &pl, uint32_t c) {
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     const uint32_t so = (uint32_t)panel_chunk_qs(pl.K, pl.p[t], pl.R[t], c);
@@ -72,7 +74,7 @@ __device__ inline void load_chunk(Chunk<P> &b, const Plan<P> &pl, uint32_t c) {
         pl.ws, pl.s_voff[t], (uint32_t)panel_chunk_sc(pl.K, pl.p[t], pl.R[t], c) * 2, 0);
   }
 #pragma unroll
-  for (int i = 0; i < 8; ++i)
+  for (int i = 0; i < XR / 4; ++i)
     b.x[i] = __builtin_bit_cast(
         f32x4, __builtin_amdgcn_raw_buffer_load_b128(pl.xr, pl.x_voff + i * 16 * pl.K, c * kChunkK * 4, 0));
 }
@@ -87,20 +89,21 @@ __device__ inline uint32_t x_piece(uint32_t row, uint32_t j) {
 
 // acc[t] += W_t(chunk) . X(chunk)^T over the four k-steps; step s uses half
 // (s & 1) of weight unit s >> 1 and activation piece 4h + s of row c.
-template <int P>
-__device__ inline void accumulate(const Chunk<P> &b, uint8_t *xt, uint32_t lane,
+template <int P, int XR>
+__device__ inline void accumulate(const Chunk<P, XR> &b, uint8_t *xt, uint32_t lane,
                                   f32x16 (&acc)[P]) {
   const uint32_t h = lane >> 5, c = lane & 31;
   // stage: f32 -> f16 (round to nearest even, the kCvt32 staging), 8 bytes per piece
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < XR / 4; ++i) {
     const uint32_t row = 4 * i + (lane >> 4), k4 = lane & 15;  // floats 4*k4 .. +3
     const f16x4 v = {(f16)b.x[i].x, (f16)b.x[i].y, (f16)b.x[i].z, (f16)b.x[i].w};
     *reinterpret_cast<f16x4 *>(xt + x_piece(row, k4 >> 1) + (k4 & 1) * 8) = v;
   }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    const f16x8 xf = *reinterpret_cast<const f16x8 *>(xt + x_piece(c, 4 * h + s));
+    f16x8 xf = {};
+    if (XR == 32 || c < XR) xf = *reinterpret_cast<const f16x8 *>(xt + x_piece(c, 4 * h + s));
 #pragma unroll
     for (int t = 0; t < P; ++t) {
       const f16x2 s2 = {__builtin_bit_cast(f16, (uint16_t)b.s[t]),
@@ -115,50 +118,45 @@ __device__ inline void accumulate(const Chunk<P> &b, uint8_t *xt, uint32_t lane,
   }
 }
 
-struct SkinnyArgs {
-  float *out;
-  const float *x;
-  const uint8_t *qs;
-  const f16 *sc;
-  uint32_t m, n, k;
-  uint32_t groups, slices;  // panel groups (P panels each) and 32-row activation slices
-  // split K over `splits` workgroups per (group, slice): partial tiles in `ws`,
-  // arrival counters in `cnt` (zero between uses)
-  uint32_t splits;
-  f32x4 *ws;
-  uint32_t *cnt;
-};
 
-// LDS: the four waves' activation tiles during the K loop, then the partial
-// sums of the reduction
-template <int P, int KW>
+// LDS: the waves' activation tiles (XR rows x 128 bytes) during the K loop,
+// then the partial sums of the reduction
+template <int P, int KW, int XR>
 constexpr int skinny_lds() {
-  return (KW * 4096 > KW * P * 4 * 64 * 16) ? KW * 4096 : KW * P * 4 * 64 * 16;
+  return (KW * XR * 128 > KW * P * 4 * 64 * 16) ? KW * XR * 128 : KW * P * 4 * 64 * 16;
 }
 
-// P panels per workgroup, KW waves splitting K
-template <int P, int KW, int WPE>
-__global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void q8_skinny_kernel(
-    SkinnyArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[skinny_lds<P, KW>()];
+// P panels per workgroup, KW waves splitting K, XR activation rows loaded per
+// slice, WIN chunks in flight per wave.
+//
+// Grid (x, y, z) = (panel group, 32-row activation slice, K split).  The
+// arguments are scalars in the order the kernel first needs them, so the
+// leading ones arrive preloaded in SGPRs, and the set-up has no integer
+// division: split s covers chunks [s * cper + min(s, crem), + cper + (s <
+// crem)).  `out`: f32 [m][n]; `ws`, `cnt`: partial tiles and arrival counters
+// (zero between uses) when K is split.
+template <int P, int KW, int XR, int WIN>
+__global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 > 2 ? KW / 4 : 2))) void q8_skinny_kernel(
+    const uint8_t *__restrict__ qs, const f16 *__restrict__ sc, const float *__restrict__ x,
+    uint32_t M, uint32_t N, uint32_t K, uint32_t cper, uint32_t crem, uint32_t groups,
+    float *__restrict__ out, f32x4 *ws, uint32_t *cnt) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[skinny_lds<P, KW, XR>()];
 
-  // Consecutive workgroups go to different XCDs (round-robin).  Map the
-  // slices of one panel group to one XCD so they share its weights in that
-  // L2: workgroup b runs on XCD b % 8 and takes group 8 * ((b / 8) / S) + b % 8,
-  // slice (b / 8) % S; split K ranges are the slowest index.
-  const uint32_t per_split = (a.groups + 7) / 8 * 8 * a.slices;
-  const uint32_t split = blockIdx.x / per_split, b = blockIdx.x % per_split, S = a.slices;
-  const uint32_t grp = 8 * ((b / 8) / S) + b % 8, slice = (b / 8) % S;
-  if (grp >= a.groups) return;
+  // Consecutive workgroups go to different XCDs (round-robin, x fastest).
+  // The grid's x extent is a multiple of 8, so every slice and K split of
+  // panel group g runs on XCD g % 8 and shares its weights in that L2.
+  const uint32_t grp = blockIdx.x, slice = blockIdx.y, split = blockIdx.z;
+  if (grp >= groups) return;
+  const uint32_t splits = gridDim.z;
 
-  const uint32_t K = a.k, C = K / kChunkK;
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
-  const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
-  // this workgroup's K chunks [cs, ce), split KW ways over the waves
-  const uint32_t cs = split * C / a.splits, ce = (split + 1) * C / a.splits;
-  const uint32_t c0 = cs + (wave * (ce - cs)) / KW, c1 = cs + ((wave + 1) * (ce - cs)) / KW;
+  const uint32_t np = (N + kPanelRows - 1) / kPanelRows;
+  // this workgroup's K chunks [cs, cs + nck), split KW ways over the waves
+  const uint32_t cs = split * cper + (split < crem ? split : crem);
+  const uint32_t nck = cper + (split < crem ? 1 : 0);
+  const uint32_t c0 = cs + (wave * nck) / KW, c1 = cs + ((wave + 1) * nck) / KW;
 
   // Panels past N are clamped to the last one and lanes past a partial
   // panel's last row read row R-1 (in bounds; their sums are never stored).
@@ -166,37 +164,37 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   // M read zeros.
   Plan<P> pl;
   pl.K = K;
-  pl.wq = make_rsrc(a.qs, a.n * K);
-  pl.ws = make_rsrc(a.sc, a.n * (K / 32) * 2);
+  pl.wq = make_rsrc(qs, N * K);
+  pl.ws = make_rsrc(sc, N * (K / 32) * 2);
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     const uint32_t pp = grp * P + t < np ? grp * P + t : np - 1;
     pl.p[t] = pp;
-    pl.R[t] = panel_rows(a.n, pp);
+    pl.R[t] = panel_rows(N, pp);
     const uint32_t rr = r < pl.R[t] ? r : pl.R[t] - 1;
     pl.w_voff[t] = (h * pl.R[t] + rr) * 16;
     pl.s_voff[t] = (h * pl.R[t] + rr) * 2;
   }
   const uint32_t m0 = slice * kSlice;
-  const uint32_t rows = a.m - m0 < kSlice ? a.m - m0 : kSlice;
-  pl.xr = make_rsrc(a.x + (size_t)m0 * K, rows * K * 4);
+  const uint32_t rows = M - m0 < kSlice ? M - m0 : kSlice;
+  pl.xr = make_rsrc(x + (size_t)m0 * K, rows * K * 4);
   pl.x_voff = (lane >> 4) * K * 4 + (lane & 15) * 16;
 
-  uint8_t *xt = smem + wave * 4096;
-  Chunk<P> win[kWin];
+  uint8_t *xt = smem + wave * XR * 128;
+  Chunk<P, XR> win[WIN];
 #pragma unroll
-  for (int i = 0; i < kWin; ++i)
-    if (c0 + i < c1) load_chunk<P>(win[i], pl, c0 + i);
+  for (int i = 0; i < WIN; ++i)
+    if (c0 + i < c1) load_chunk<P, XR>(win[i], pl, c0 + i);
   f32x16 acc[P];
 #pragma unroll
   for (int t = 0; t < P; ++t) acc[t] = (f32x16){};
 #pragma unroll 1
-  for (uint32_t c = c0; c < c1; c += kWin) {
+  for (uint32_t c = c0; c < c1; c += WIN) {
 #pragma unroll
-    for (int i = 0; i < kWin; ++i) {
+    for (int i = 0; i < WIN; ++i) {
       if (c + i < c1) {
-        accumulate<P>(win[i], xt, lane, acc);
-        if (c + i + kWin < c1) load_chunk<P>(win[i], pl, c + i + kWin);
+        accumulate<P, XR>(win[i], xt, lane, acc);
+        if (c + i + WIN < c1) load_chunk<P, XR>(win[i], pl, c + i + WIN);
       }
     }
   }
@@ -222,49 +220,49 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
       for (int w = 1; w < KW; ++w) v[t] += red[((w * P + t) * 4 + wave) * 64 + lane];
     }
   }
-  if (a.splits > 1) {
+  if (splits > 1) {
     // Split K: each workgroup writes its partial tile through to memory
     // (device-scope sc1 stores) and counts itself in; the last to arrive adds
     // the splits' partials in split order and stores the rows.
     __shared__ uint32_t arrived;
     constexpr int kSc1 = 16;
-    const uint32_t tile = grp * a.slices + slice;
+    const uint32_t tile = grp * gridDim.y + slice;
     const uint32_t part = P * 4 * 64 * 16;  // bytes per partial tile
-    const __amdgpu_buffer_rsrc_t wsr = make_rsrc(a.ws, a.groups * a.slices * a.splits * part);
+    const __amdgpu_buffer_rsrc_t wsr = make_rsrc(ws, groups * gridDim.y * splits * part);
     if (wave < 4) {
 #pragma unroll
       for (int t = 0; t < P; ++t)
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v[t]), wsr,
                                                ((t * 4 + wave) * 64 + lane) * 16,
-                                               (tile * a.splits + split) * part, kSc1);
+                                               (tile * splits + split) * part, kSc1);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (threadIdx.x == 0)
-      arrived = __hip_atomic_fetch_add(&a.cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      arrived = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
-    if (arrived != a.splits - 1) return;
+    if (arrived != splits - 1) return;
     if (wave < 4) {
 #pragma unroll
       for (int t = 0; t < P; ++t) {
         v[t] = (f32x4){0.0f, 0.0f, 0.0f, 0.0f};
-        for (uint32_t s2 = 0; s2 < a.splits; ++s2)
+        for (uint32_t s2 = 0; s2 < splits; ++s2)
           v[t] += __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
                                                 wsr, ((t * 4 + wave) * 64 + lane) * 16,
-                                                (tile * a.splits + s2) * part, kSc1));
+                                                (tile * splits + s2) * part, kSc1));
       }
     }
     if (threadIdx.x == 0)
-      __hip_atomic_store(&a.cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
   const uint32_t m = m0 + r;
-  if (wave >= 4 || m >= a.m) return;
+  if (wave >= 4 || m >= M) return;
   const uint32_t nl = wave * 8 + h * 4;  // panel-local row of v.x
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     if (grp * P + t >= np) break;
     const uint32_t R = pl.R[t];
-    float *o = a.out + (size_t)m * a.n + pl.p[t] * kPanelRows + nl;
+    float *o = out + (size_t)m * N + pl.p[t] * kPanelRows + nl;
     if (nl + 4 <= R) {
       o[0] = v[t].x;
       o[1] = v[t].y;
@@ -278,25 +276,56 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) 
   }
 }
 
-template <int P, int KW, int WPE>
-int launch_skinny(SkinnyArgs a) {
+// Launch shapes.  Single panels (decoder projections, 40 - 160 panels): eight
+// waves split K, three chunks in flight each, so a K = 1280 range (2 - 3
+// chunks per wave) is one round of loads.  (Sixteen waves with two chunks
+// each measured slower: a workgroup's waves start up to ~0.8 us apart and the
+// reduction waits for the last.)  Panel groups (the vocab logits, 1621
+// panels): four panels per wave share each activation load, four waves split
+// K.
+constexpr int kPanelWaves = 8, kPanelWin = 3;
+constexpr int kGroupWaves = 4, kGroupWin = 2;
+constexpr uint32_t kMaxSplits = 4;
+
+// One projection: out[m][n] = sum_k x[m][k] w[n][k].
+struct Proj {
+  float *out;
+  const float *x;
+  const uint8_t *qs;
+  const f16 *sc;
+  uint32_t m, n, k;
+};
+
+template <int P, int KW, int XR, int WIN>
+int launch_skinny(const Proj &a) {
   const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
-  a.groups = (np + P - 1) / P;
+  const uint32_t groups = (np + P - 1) / P, slices = (a.m + kSlice - 1) / kSlice;
   const uint32_t C = a.k / kChunkK;
   // Few panels and a long K (the FFN down projection, 40 panels x 80 chunks):
   // split K over up to four workgroups per tile, >= 16 chunks each.
-  a.splits = 1;
+  uint32_t splits = 1;
+  f32x4 *ws = nullptr;
+  uint32_t *cnt = nullptr;
   if (P == 1 && np < 128 && C >= 32) {
-    a.splits = C / 16 < 4 ? C / 16 : 4;
-    float *ws = nullptr;
+    splits = C / 16 < kMaxSplits ? C / 16 : kMaxSplits;
+    float *w = nullptr;
     const size_t part = (size_t)P * 4 * 64 * 16;
-    if (int rc = workspace(a.groups * a.slices * a.splits * part, a.groups * a.slices, &ws, &a.cnt))
-      return rc;
-    a.ws = reinterpret_cast<f32x4 *>(ws);
+    if (int rc = workspace(groups * slices * splits * part, groups * slices, &w, &cnt)) return rc;
+    ws = reinterpret_cast<f32x4 *>(w);
   }
-  const uint32_t grid = (a.groups + 7) / 8 * 8 * a.slices * a.splits;
-  hipLaunchKernelGGL((q8_skinny_kernel<P, KW, WPE>), dim3(grid), dim3(KW * 64), 0, stream(), a);
+  const dim3 grid((groups + 7) / 8 * 8, slices, splits);
+  hipLaunchKernelGGL((q8_skinny_kernel<P, KW, XR, WIN>), grid, dim3(KW * 64), 0, stream(), a.qs,
+                     a.sc, a.x, a.m, a.n, a.k, C / splits, C % splits, groups, a.out, ws, cnt);
   return check_launch("madi_q8_pproj");
+}
+
+// wide matrices (the vocab logits): four panels per workgroup share each
+// activation load; narrow ones keep one panel per workgroup
+template <int XR>
+int launch_rows(const Proj &a) {
+  const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
+  if (np >= 1024) return launch_skinny<4, kGroupWaves, XR, kGroupWin>(a);
+  return launch_skinny<1, kPanelWaves, XR, kPanelWin>(a);
 }
 
 }  // namespace
@@ -313,19 +342,9 @@ extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const 
   if (!aligned(qs, 16) || !aligned(scales, 2) || !aligned(in, 16) || !aligned(out, 4))
     return fail(MADI_ERR_ALIGN, "madi_q8_pproj: qs and in need 16-byte alignment");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_pproj: madi_init has not succeeded");
-  SkinnyArgs a{};
-  a.out = out;
-  a.x = in;
-  a.qs = static_cast<const uint8_t *>(qs);
-  a.sc = static_cast<const f16 *>(scales);
-  a.m = m;
-  a.n = n;
-  a.k = k;
-  a.slices = (m + kSlice - 1) / kSlice;
-  // wide matrices (the vocab logits): four panels per workgroup share each
-  // activation load; narrow ones keep one panel per workgroup and split K
-  // eight ways for parallelism
-  const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
-  if (np >= 1024) return launch_skinny<4, 4, 2>(a);
-  return launch_skinny<1, 8, 2>(a);
+  const Proj a{out, in, static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), m, n, k};
+  // a batch of up to 8 or 16 rows loads only those activation rows
+  if (m <= 8) return launch_rows<8>(a);
+  if (m <= 16) return launch_rows<16>(a);
+  return launch_rows<32>(a);
 }
