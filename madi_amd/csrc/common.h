@@ -15,6 +15,8 @@ int fail(int code, const char *fmt, ...);
 int check_launch(const char *what);
 bool initialized();
 hipStream_t stream();
+// Compute units of the device (256 on an MI355X).
+int cu_count();
 // The library's split-K workspace: `partial_bytes` of fp32 partial sums and
 // `counters` arrival counters that are zero whenever no kernel is using them.
 // Grows on demand (a grow waits for the device); freed by madi_cleanup.

@@ -738,10 +738,20 @@ extern "C" int madi_q8_gemm(const void *a, const void *qs, const void *scales, v
   const f16 *S = static_cast<const f16 *>(scales);
   f16 *C = static_cast<f16 *>(c);
   if (m <= 32) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k);
-  // 128-row tiles, unless they would split K: then 64-row tiles, which halve
-  // the split count and the partial sums through memory (fc2 at M = 1500:
-  // 2 splits of 40 chunks instead of 4 of 20, 35 -> 30.5 us)
-  if (m <= 64 || split_count(tile_count(m, n, 4), k / kChunkK) > 1)
+  if (m <= 64) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k);
+  // Where 128-row tiles would split K: 64-row tiles, which halve the split
+  // count and the partial sums through memory (fc2 at M = 1500: 2 splits of
+  // 40 chunks instead of 4 of 20, 35 -> 30.5 us).
+  if (split_count(tile_count(m, n, 4), k / kChunkK) > 1)
     return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k);
+  // Otherwise the lowest tiles whose count still fits one workgroup per CU:
+  // a lower tile does less MFMA work per byte loaded (a 32-row tile takes
+  // ~0.9x the time of a 64-row one for half the work) but spreads over more
+  // CUs.  At M = 1500: out 1280->1280 60 -> 235 tiles (16.8 -> 11.3 us),
+  // cross K,V 1280->2560 120 -> 240 tiles (18.2 -> 13.9 us); q,k,v
+  // 1280->3840 (180 tiles) and fc1 (240) keep 128 rows.
+  const uint32_t cus = (uint32_t)cu_count();
+  if (tile_count(m, n, 1) <= cus) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k);
+  if (tile_count(m, n, 2) <= cus) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k);
   return dispatch_epi<4>(epilogue, A, Q, S, C, bias, m, n, k);
 }

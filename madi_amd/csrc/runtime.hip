@@ -79,6 +79,7 @@ int check_launch(const char *what) {
 }
 
 bool initialized() { return g_init; }
+int cu_count() { return g_cu_count; }
 hipStream_t stream() { return g_stream; }
 
 }  // namespace madi

@@ -167,20 +167,34 @@ def test_gemm_parity_small(q, m, n, k):
     assert tight_ok(c, a, qs, sc)
 
 
+def tile_rows(m):
+    """Rows at every 32-row boundary of an m-row GEMM and a random sample."""
+    edges = np.arange(0, m, 32)
+    rows = np.r_[edges, edges - 1, m - 1, np.random.default_rng(m).integers(0, m, 8)]
+    return np.unique(rows[(rows >= 0) & (rows < m)])
+
+
+# One shape per m-tile height on a 256-CU device: 32-row tiles (m = 20, and
+# m = 130, where 32-row tiles still fit one workgroup per CU), 64-row tiles
+# (m = 33) and 128-row tiles (m = 520 at n = 8192: 64-row tiles would be 288
+# workgroups).
+TILE_SHAPES = [(20, 320), (33, 320), (130, 320), (520, 8192)]
+
+
 @pytest.mark.parametrize("k", [128, 256, 320, 512, 768, 1024])
-@pytest.mark.parametrize("m", [20, 33, 130])
-def test_gemm_k_loop_shapes(q, m, k):
-    """Every K-loop shape at each m-tile height (32, 64, 128 rows): chunk counts
-    below eight or not a multiple of four run the padded loop (2, 4, 5
-    chunks); 8 chunks is one full trip plus the peeled last trip, 12 and 16
-    two and three trips."""
-    n = 320
+@pytest.mark.parametrize("m,n", TILE_SHAPES)
+def test_gemm_k_loop_shapes(q, m, n, k):
+    """Every K-loop shape at each m-tile height: chunk counts below eight or
+    not a multiple of four run the padded loop (2, 4, 5 chunks); 8 chunks is
+    one full trip plus the peeled last trip, 12 and 16 two and three trips."""
     say(f"gemm k-loop m={m} n={n} k={k}")
     a, qs, sc = synth.gemm_case(m * 13 + k, m, n, k)
     c = _gemm(q, a, qs, sc)
-    ref = O.q8_gemm_rows(a, qs, sc, threads=8)
-    assert normwise(c, ref) <= TOL, normwise(c, ref)
-    assert tight_ok(c, a, qs, sc)
+    rows = tile_rows(m)
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, threads=8)
+    assert normwise(c[rows], ref) <= TOL, normwise(c[rows], ref)
+    assert tight_ok(c[rows], a[rows], qs, sc)
+    assert np.all(np.isfinite(c))
 
 
 @pytest.mark.parametrize("m,n,k", [
@@ -216,17 +230,20 @@ def test_gemm_one_hot_is_dequant(q):
     assert np.array_equal(c.view(np.uint16), ref.view(np.uint16))
 
 
+@pytest.mark.parametrize("m,n", TILE_SHAPES)
 @pytest.mark.parametrize("gelu", [False, True])
-def test_gemm_bias_epilogues(q, gelu):
-    say(f"gemm bias gelu={gelu}")
-    m, n, k = 200, 768, 640
+def test_gemm_bias_epilogues(q, gelu, m, n):
+    k = 640
+    say(f"gemm bias gelu={gelu} m={m} n={n} k={k}")
     a, qs, sc = synth.gemm_case(11, m, n, k)
     bias = np.random.default_rng(12).standard_normal(n).astype(np.float32)
     c = _gemm(q, a, qs, sc, bias=bias, gelu=gelu)
-    ref = O.q8_gemm_rows(a, qs, sc, bias=bias,
+    rows = tile_rows(m)
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, bias=bias,
                          epilogue=O.EPI_BIAS_GELU if gelu else O.EPI_BIAS, threads=8)
-    assert normwise(c, ref) <= TOL
-    assert tight_epi_ok(c, a, qs, sc, bias, gelu)
+    assert normwise(c[rows], ref) <= TOL
+    assert tight_epi_ok(c[rows], a[rows], qs, sc, bias, gelu)
+    assert np.all(np.isfinite(c))
 
 
 @pytest.mark.parametrize("name,n,k", [("fc1", 5120, 1280), ("fc2", 1280, 5120), ("qkv", 3840, 1280)])
