@@ -549,6 +549,27 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
       arrived = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
     if (arrived != splits - 1) return;
+    constexpr int kGroups = 2 * MT * 4;  // register groups q = (t, i, g) in order
+    if (MT <= 2 && splits == 2) {
+      // Two splits (fc2-like shapes at 64-row tiles): the wave's whole share
+      // of the other partial (2 * MT * 4 KiB) in flight at once, one memory
+      // latency; own + other is exact in either order.
+      const uint32_t other = split ^ 1u;
+      f32x4 o[kGroups];
+#pragma unroll
+      for (int q = 0; q < kGroups; ++q)
+        o[q] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(wsr, ((wave * kGroups + q) * 64 + lane) * 16,
+                                                         (tile * splits + other) * kPart, kSc1));
+#pragma unroll
+      for (int q = 0; q < kGroups; ++q) {
+        const int t = q / (MT * 4), i = (q / 4) % MT, g = q % 4;
+        acc[t][i][4 * g] += o[q].x;
+        acc[t][i][4 * g + 1] += o[q].y;
+        acc[t][i][4 * g + 2] += o[q].z;
+        acc[t][i][4 * g + 3] += o[q].w;
+      }
+    } else {
     // Sum the splits' partials in split order, this workgroup's own from its
     // registers at its own position, so the result does not depend on which
     // workgroup arrives last.  One fully unrolled pass over the register
@@ -567,9 +588,9 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
       rs[s2] = s2 < splits && s2 != split ? wsr : zr;
       mine[s2] = s2 == split ? 1.0f : 0.0f;
     }
-    // register groups q = (t, i, g) in order; group q + kAhead's loads are
-    // issued before group q is summed, so the waits only cover old loads
-    constexpr int kGroups = 2 * MT * 4, kAhead = 6;
+    // group q + kAhead's loads are issued before group q is summed, so the
+    // waits only cover old loads
+    constexpr int kAhead = 6;
     auto load_group = [&](int q, f32x4 (&dst)[kMaxSplits]) {
       const uint32_t voff = ((wave * kGroups + q) * 64 + lane) * 16;
 #pragma unroll
@@ -597,6 +618,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
       acc[t][i][4 * g + 2] = sum.z;
       acc[t][i][4 * g + 3] = sum.w;
       __builtin_amdgcn_sched_barrier(0);
+    }
     }
     if (threadIdx.x == 0)  // ready for the next launch
       __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
