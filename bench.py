@@ -20,7 +20,9 @@ cores (a reported baseline only).
 Beside the headline, "configs" reports the other measured workloads: the
 encoder GEMM set of one 30 s window (32 layers, independent weights), a
 batched decode step at M = 8 and 16 (skinny Q8 projections, cold weights) with
-the per-chunk cross-attention K|V GEMM, and the 16-window long-audio fc1/fc2.
+the per-chunk cross-attention K|V GEMM, one decoder token at M = 1 through the
+GEMV family (and its fused q|k|v GEMV alone), and the 16-window long-audio
+fc1/fc2.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-configs]
        python bench.py --calibrate-copy   (a plain 256 MiB device copy, the
@@ -249,6 +251,82 @@ def config_batched_decode(torch, stream, q8, reps=20):
     return res
 
 
+def config_decode_token(torch, stream, q8, reps=20):
+    """One decoder token at M = 1 through the GEMV family with the reference
+    decodeBlock's Q8 calls (decoder.zig:260-309): per layer the fused q|k|v
+    GEMV 1280->3840 with the K/V cache store, out 1280->1280, cross-q + bias,
+    cross-out, FFN-up + bias + GELU 1280->5120, FFN-down + bias + residual
+    5120->1280; then the vocab logits 1280->51866 (transcribe.zig:4369).  Two
+    alternating weight sets (2 x 168 MB > the 256 MB Infinity Cache).  Also
+    the q|k|v GEMV alone over 64 rotating copies (315 MB), cold."""
+    d, mlp = DIM, 5120
+    rng = np.random.default_rng(105)
+    f32 = lambda *shape: torch.from_numpy(rng.standard_normal(shape).astype(np.float32)).cuda()
+    x, xb, q, ao, mo, mh = f32(mlp), f32(d), f32(d), f32(d), f32(d), f32(mlp)
+    qb, vb, bd, bm = f32(d), f32(d), f32(d), f32(mlp)
+    kc, vc = f32(448, d), f32(448, d)
+    pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+    logits = torch.empty(VOCAB, dtype=torch.float32, device="cuda")
+    shapes = [(3 * d, d), (d, d), (d, d), (d, d), (mlp, d), (d, mlp)]
+    sets = []
+    for s_ in range(2):
+        layers = [[_upload_layer(q8, 4000 + 100 * s_ + 8 * l + j, n, k)
+                   for j, (n, k) in enumerate(shapes)] for l in range(DEC_LAYERS)]
+        sets.append((layers, _upload_layer(q8, 4900 + s_, VOCAB, DIM)))
+    step_bytes = (DEC_LAYERS * sum(n * k + n * (k // 32) * 2 for n, k in shapes)
+                  + VOCAB * DIM + VOCAB * (DIM // 32) * 2)
+
+    def token(i):
+        layers, vocab = sets[i % 2]
+        for w in layers:
+            q8.kQkv(q, xb, w[0], qb, vb, kc, vc, pos, d)
+            q8.kGemvQ8(mo, ao, w[1], d, d)
+            q8.kGemvQ8Bias(q, xb, w[2], bd, d, d)
+            q8.kGemvQ8(mo, ao, w[3], d, d)
+            q8.kGemvQ8BiasEpi("gemv_q8_bias_gelu", mh, xb, w[4], bm, mlp, d)
+            q8.kGemvQ8BiasEpi("gemv_q8_bias_res", x, mh, w[5], bd, d, mlp)
+        q8.kLogitGemv(logits, vocab.qs, vocab.scales, xb, VOCAB, DIM)
+
+    token(0)
+    token(1)
+    t = _timed(torch, stream, token, reps)
+    graphs = []
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    for s_ in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(g, stream=side):
+                q8.init(side)
+                token(s_)
+        graphs.append(g)
+    q8.init(stream)
+    torch.cuda.synchronize()
+    tg = _timed(torch, stream, lambda i: graphs[i % 2].replay(), reps)
+    del graphs
+    res = {"workload": "decoder token at M = 1: 4 layers x (q|k|v + K/V store 1280->3840, out, "
+                       "cross-q + bias, cross-out 1280->1280, FFN-up + bias + GELU 1280->5120, "
+                       "FFN-down + bias + residual 5120->1280) + vocab logits 1280->51866, GEMV "
+                       "family, f32 activations, weights cold (two alternating sets)",
+           "weight_bytes_per_token": step_bytes,
+           "us_per_token": round(t * 1e6, 2), "gbs": round(step_bytes / t / 1e9, 1),
+           "frac_hbm_peak": round(step_bytes / t / 1e9 / PEAK_HBM_GBS, 4),
+           "us_per_token_graph": round(tg * 1e6, 2),
+           "frac_hbm_peak_graph": round(step_bytes / tg / 1e9 / PEAK_HBM_GBS, 4)}
+    del sets
+    base = _upload_layer(q8, 4990, 3 * d, d)
+    ws = []
+    for _ in range(64):  # distinct device copies of one weight
+        tq, ts = (t_.clone() for t_ in base._keep)
+        ws.append(q8.Q8(tq.data_ptr(), ts.data_ptr(), (tq, ts)))
+    q8.kQkv(q, xb, ws[0], qb, vb, kc, vc, pos, d)
+    tq = _timed(torch, stream, lambda i: q8.kQkv(q, xb, ws[i % 64], qb, vb, kc, vc, pos, d), 64)
+    qb_bytes = 3 * d * d + 3 * d * (d // 32) * 2
+    res["qkv_gemv"] = {"us": round(tq * 1e6, 2), "gbs": round(qb_bytes / tq / 1e9, 1),
+                       "frac_hbm_peak": round(qb_bytes / tq / 1e9 / PEAK_HBM_GBS, 4)}
+    return res
+
+
 def config_long_audio(torch, stream, q8, reps=5):
     """16 stacked 30 s windows: fc1 M=24000 K=1280 N=5120 and fc2 M=24000
     K=5120 N=1280 Q8 GEMMs."""
@@ -419,6 +497,8 @@ def main():
         cfg = {"encoder_window": config_encoder_window(torch, stream, q8)}
         log("batched decode (M=8, 16)")
         cfg["batched_decode"] = config_batched_decode(torch, stream, q8)
+        log("decoder token (M=1, GEMV family)")
+        cfg["decode_token"] = config_decode_token(torch, stream, q8)
         log("long audio (M=24000)")
         cfg["long_audio"] = config_long_audio(torch, stream, q8)
         result["configs"] = cfg

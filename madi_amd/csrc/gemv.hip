@@ -4,7 +4,8 @@
 // (engine/metal/kernels/graph_helpers.metal:320-558).  The reference runs one
 // 32-lane simdgroup per output row reading char4 + float4; here a 256-thread
 // workgroup owns one 32-row panel of the panel layout and its four waves split
-// K.  Every wave64 load instruction moves one contiguous KiB (16 bytes per
+// K (sixteen waves for the decoder's 40 - 160-panel matrices, so that a
+// K = 1280 range is one round of loads).  Every wave64 load instruction moves one contiguous KiB (16 bytes per
 // lane, lane (h, r) receiving 16 weights of row r in quantisation block h),
 // issued as a buffer load with the panel/chunk offset in an SGPR.  Each wave
 // streams its K range through a two-chunk window (use chunk c, refill with
@@ -30,7 +31,13 @@ using namespace madi;
 
 namespace {
 
-constexpr int kWaves = 4;          // K quarters per panel
+// Waves per workgroup (K ranges per panel): four for wide matrices (the
+// vocab logits: 1621 panels, seven workgroups per CU); sixteen below
+// kWidePanels, where four waves would each walk five chunks of a K = 1280
+// row through the window (three rounds of memory latency) on fewer than
+// half the CUs.
+constexpr int kWaves = 4, kWavesNarrow = 16;
+constexpr uint32_t kWidePanels = 256;
 // Chunks in flight per wave, a sliding window: two keeps ~26 MB of the vocab
 // matrix in flight across the GPU, enough to cover HBM latency, while the
 // texture queues stay short enough that the activation vector (loaded first)
@@ -59,10 +66,10 @@ struct GemvArgs {
   uint32_t *cnt;
 };
 
-// LDS bytes: x (K elements of XT), the wave partials
-template <typename XT>
+// LDS bytes: x (K elements of XT), the KW waves' partials
+template <typename XT, int KW>
 constexpr size_t lds_bytes(uint32_t k) {
-  return (size_t)k * sizeof(XT) + kWaves * 32 * 4;
+  return (size_t)k * sizeof(XT) + KW * 32 * 4;
 }
 
 // One chunk's loads for a lane: its two 16-byte units and its block's scale.
@@ -128,13 +135,13 @@ __device__ inline void accumulate(const ChunkW &b, uint32_t c, const XT *xs, uin
   acc = __builtin_fmaf(part, (float)__builtin_bit_cast(f16, (uint16_t)b.s), acc);
 }
 
-template <typename XT, int MODE>
+template <typename XT, int MODE, int KW>
 //
 // Grid (x, y) = (panel, K split).  The arguments are scalars in the order the
 // kernel first needs them, so the leading ones arrive preloaded in SGPRs, and
 // the set-up has no integer division: split s covers chunks [s * cper +
 // min(s, crem), + cper + (s < crem)).
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q8_gemv_kernel(
+__global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(7))) void q8_gemv_kernel(
     const uint8_t *qs, const f16 *sc, const void *x, uint32_t n, uint32_t k, uint32_t cper,
     uint32_t crem, float *out, const float *bias, float *wsp, uint32_t *cnt, const float *qb,
     const float *vb, float *kc, float *vc, const uint32_t *pos) {
@@ -142,7 +149,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t K = a.k;
   XT *xs = reinterpret_cast<XT *>(smem);                        // [K]
-  float *red = reinterpret_cast<float *>(smem + lds_bytes<XT>(K) - kWaves * 32 * 4);  // [4][32]
+  float *red = reinterpret_cast<float *>(smem + lds_bytes<XT, KW>(K) - KW * 32 * 4);  // [KW][32]
 
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -150,10 +157,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   const uint32_t p = blockIdx.x, split = blockIdx.y;
   const uint32_t R = panel_rows(a.n, p);
   const bool live = r < R;
-  // this workgroup's K chunks [cs, cs + nck), split four ways over the waves
+  // this workgroup's K chunks [cs, cs + nck), split KW ways over the waves
   const uint32_t cs = split * cper + (split < crem ? split : crem);
   const uint32_t nck = cper + (split < crem ? 1 : 0);
-  const uint32_t c0 = cs + (wave * nck) / kWaves, c1 = cs + ((wave + 1) * nck) / kWaves;
+  const uint32_t c0 = cs + (wave * nck) / KW, c1 = cs + ((wave + 1) * nck) / KW;
 
   // ---- x: load first (16 bytes per thread and piece), then the weights.
   // Lanes past a partial panel's last row read row R-1 (in bounds; their sums
@@ -161,7 +168,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   const uint32_t pieces = K * sizeof(XT) / 16;
   const rsrc_t xr = make_rsrc(a.x, K * sizeof(XT));
   u32x4 xv0 = {}, xv1 = {};
-  const uint32_t i0 = threadIdx.x, i1 = threadIdx.x + 256;
+  const uint32_t i0 = threadIdx.x, i1 = threadIdx.x + KW * 64;
   if (i0 < pieces) xv0 = __builtin_amdgcn_raw_buffer_load_b128(xr, i0 * 16, 0, 0);
   if (i1 < pieces) xv1 = __builtin_amdgcn_raw_buffer_load_b128(xr, i1 * 16, 0, 0);
 
@@ -184,7 +191,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   }
 
   // stage x
-  for (uint32_t i = threadIdx.x; i < pieces; i += 256) {
+  for (uint32_t i = threadIdx.x; i < pieces; i += KW * 64) {
     const u32x4 v =
         i == i0 ? xv0 : (i == i1 ? xv1 : __builtin_amdgcn_raw_buffer_load_b128(xr, i * 16, 0, 0));
     reinterpret_cast<u32x4 *>(xs)[i] = v;
@@ -216,7 +223,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(7))) void q
   __syncthreads();
   const uint32_t t = threadIdx.x;
   float v = 0.0f;
-  if (t < 32) v = red[t] + red[32 + t] + red[64 + t] + red[96 + t];
+  if (t < 32) {  // the waves' partials in wave order
+    v = red[t];
+#pragma unroll
+    for (int w = 1; w < KW; ++w) v += red[w * 32 + t];
+  }
   if (a.splits > 1) {
     // Split K: each workgroup writes its 32 partial row sums through to memory
     // (system-scope stores) and counts itself in; the last to arrive adds the
@@ -281,10 +292,16 @@ int launch(const char *what, const GemvArgs &a) {
     b.splits = C / 16 < 4 ? C / 16 : 4;
     if (int rc = workspace((size_t)np * b.splits * 32 * 4, np, &b.ws, &b.cnt)) return rc;
   }
-  const size_t lds = lds_bytes<XT>(a.k);
-  hipLaunchKernelGGL((q8_gemv_kernel<XT, MODE>), dim3(np, b.splits), dim3(256), lds, stream(),
-                     b.qs, b.sc, b.x, b.n, b.k, C / b.splits, C % b.splits, b.out, b.bias, b.ws,
-                     b.cnt, b.qb, b.vb, b.kc, b.vc, b.pos);
+  if (np >= kWidePanels)
+    hipLaunchKernelGGL((q8_gemv_kernel<XT, MODE, kWaves>), dim3(np, b.splits), dim3(kWaves * 64),
+                       (lds_bytes<XT, kWaves>(a.k)), stream(), b.qs, b.sc, b.x, b.n, b.k,
+                       C / b.splits, C % b.splits, b.out, b.bias, b.ws, b.cnt, b.qb, b.vb, b.kc,
+                       b.vc, b.pos);
+  else
+    hipLaunchKernelGGL((q8_gemv_kernel<XT, MODE, kWavesNarrow>), dim3(np, b.splits),
+                       dim3(kWavesNarrow * 64), (lds_bytes<XT, kWavesNarrow>(a.k)), stream(), b.qs,
+                       b.sc, b.x, b.n, b.k, C / b.splits, C % b.splits, b.out, b.bias, b.ws, b.cnt,
+                       b.qb, b.vb, b.kc, b.vc, b.pos);
   return check_launch(what);
 }
 
