@@ -190,6 +190,25 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(7))) vo
     load_chunk(win[k], in ? wq : wz, in ? ws : wz, K, c0 + k, p, R, w_voff, s_voff);
   }
 
+  // The epilogue's operands (bias, residual, q/v bias, cache position) load
+  // now, behind the weights, so their latency passes during the K loop
+  // instead of after it.  Lanes 0..R-1 of wave 0 own the panel's rows.
+  const uint32_t erow = p * kPanelRows + threadIdx.x;
+  float e_bias = 0.0f, e_res = 0.0f;
+  uint32_t e_pos = 0;
+  if (threadIdx.x < R) {
+    if constexpr (MODE == kBias || MODE == kBiasGelu) {
+      e_bias = a.bias[erow];
+    } else if constexpr (MODE == kBiasRes) {
+      e_bias = a.bias[erow];
+      e_res = a.out[erow];
+    } else if constexpr (MODE == kQkv) {
+      if (erow < a.k) e_bias = a.qb[erow];
+      else if (erow >= 2 * a.k) e_bias = a.vb[erow - 2 * a.k];
+    }
+  }
+  if constexpr (MODE == kQkv) e_pos = a.pos[0];
+
   // stage x
   for (uint32_t i = threadIdx.x; i < pieces; i += KW * 64) {
     const u32x4 v =
@@ -251,23 +270,23 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(7))) vo
     if (t == 0) __hip_atomic_store(&a.cnt[p], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
   if (t >= R) return;
-  const uint32_t nrow = p * kPanelRows + t;
+  const uint32_t nrow = erow;  // t == threadIdx.x
   if constexpr (MODE == kPlain) {
     a.out[nrow] = v;
   } else if constexpr (MODE == kBias) {
-    a.out[nrow] = v + a.bias[nrow];
+    a.out[nrow] = v + e_bias;
   } else if constexpr (MODE == kBiasGelu) {
-    a.out[nrow] = gelu_erf(v + a.bias[nrow]);
+    a.out[nrow] = gelu_erf(v + e_bias);
   } else if constexpr (MODE == kBiasRes) {
-    a.out[nrow] = a.out[nrow] + v + a.bias[nrow];
+    a.out[nrow] = e_res + v + e_bias;
   } else {  // kQkv: a.n = 3D, a.k = D
-    const uint32_t D = a.k, pos = a.pos[0];
+    const uint32_t D = a.k, pos = e_pos;
     if (nrow < D)
-      a.out[nrow] = v + a.qb[nrow];
+      a.out[nrow] = v + e_bias;
     else if (nrow < 2 * D)
       a.kc[(size_t)pos * D + (nrow - D)] = v;
     else
-      a.vc[(size_t)pos * D + (nrow - 2 * D)] = v + a.vb[nrow - 2 * D];
+      a.vc[(size_t)pos * D + (nrow - 2 * D)] = v + e_bias;
   }
 }
 
