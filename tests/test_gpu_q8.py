@@ -277,7 +277,12 @@ def test_gemm_large_m(q):
 
 
 # ------------------------------------------------------------------ GEMV
-@pytest.mark.parametrize("n,k", [(51866, 1280), (3840, 1280), (1280, 5120), (5120, 1280), (40, 64)])
+# (51866, 1280): four waves per panel; the others sixteen: (3840, 1280),
+# (5120, 1280), (40, 64) one or two chunks per wave, (1280, 5120) four K
+# splits, (5120, 4096) four chunks per wave through the two-chunk window,
+# (40, 12288) the largest K in four splits of 48 chunks
+@pytest.mark.parametrize("n,k", [(51866, 1280), (3840, 1280), (1280, 5120), (5120, 1280), (40, 64),
+                                 (5120, 4096), (40, 12288)])
 def test_gemv_parity(q, n, k):
     say(f"gemv n={n} k={k}")
     x16, qs, sc = synth.gemv_case(n + k, n, k)
