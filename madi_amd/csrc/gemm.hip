@@ -623,29 +623,46 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
     if (threadIdx.x == 0)  // ready for the next launch
       __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
+  // The tile leaves through LDS one m-tile (32 rows) at a time: all waves
+  // write their columns of m-tile i, meet, and each stores 8 of its rows
+  // while the next m-tile is converted, so the stores (the HBM write rate
+  // bounds them: every workgroup writes at once) start after a quarter of
+  // the conversion instead of all of it.  A store instruction writes two
+  // rows (512 B each): lane (h, r) writes 16 bytes of row 2j + h at column
+  // 8r.  The stores write through the L2 (sc1), so the tile leaves no dirty
+  // lines for the end-of-kernel release to write back after the last
+  // workgroup; rows past M fall outside the tile's buffer resource and are
+  // dropped, columns past N are skipped per lane.
   uint8_t *Ct = smem;
+  const uint32_t n = p0 * kPanelRows + r * 8;
+  const uint32_t rows = M - m0 < 32 * MT ? M - m0 : 32 * MT;
+  const __amdgpu_buffer_rsrc_t cr =
+      __builtin_amdgcn_make_buffer_rsrc(Cout + (size_t)m0 * N, 0, (int)(rows * N * 2), 0x00020000);
+  f32x4 b4[2][4];
+  if constexpr (EPI != MADI_EPI_NONE) {
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const uint32_t nl = (2 * wave + t) * kPanelRows;  // tile-local column of the panel
-    f32x4 b4[4];
-    if constexpr (EPI != MADI_EPI_NONE) {
-      uint32_t p = p0 + 2 * wave + t;
-      p = p < np ? p : np - 1;  // clamped panels: bias read in bounds, result never stored
+    for (int t = 0; t < 2; ++t) {
+      uint32_t pb = p0 + 2 * wave + t;
+      pb = pb < np ? pb : np - 1;  // clamped panels: bias read in bounds, result never stored
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        b4[g] = *reinterpret_cast<const f32x4 *>(bias + p * kPanelRows + g * 8 + h * 4);
+        b4[t][g] = *reinterpret_cast<const f32x4 *>(bias + pb * kPanelRows + g * 8 + h * 4);
     }
+  }
 #pragma unroll
-    for (int i = 0; i < MT; ++i) {
+  for (int i = 0; i < MT; ++i) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const uint32_t nl = (2 * wave + t) * kPanelRows;  // tile-local column of the panel
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         float v[4] = {acc[t][i][g * 4 + 0], acc[t][i][g * 4 + 1], acc[t][i][g * 4 + 2],
                       acc[t][i][g * 4 + 3]};
         if constexpr (EPI != MADI_EPI_NONE) {
-          v[0] += b4[g].x;
-          v[1] += b4[g].y;
-          v[2] += b4[g].z;
-          v[3] += b4[g].w;
+          v[0] += b4[t][g].x;
+          v[1] += b4[t][g].y;
+          v[2] += b4[t][g].z;
+          v[3] += b4[t][g].w;
           if constexpr (EPI == MADI_EPI_BIAS_GELU) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = gelu_erf_fast(v[e]);
@@ -655,23 +672,13 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
         *reinterpret_cast<f16x4 *>(Ct + (i * 32 + r) * kCStride + (nl + g * 8 + h * 4) * 2) = o;
       }
     }
-  }
-  __syncthreads();
-  // wave w stores tile rows [8*MT*w, 8*MT*(w+1)), two rows (512 B each) per
-  // instruction: lane (h, r) writes 16 bytes of row 2j + h at column 8r.  The
-  // stores write through the L2 (sc1), so the tile leaves no dirty lines for
-  // the end-of-kernel release to write back after the last workgroup; rows
-  // past M fall outside the tile's buffer resource and are dropped.
-  const uint32_t n = p0 * kPanelRows + r * 8;
-  if (n >= N) return;
-  const uint32_t rows = M - m0 < 32 * MT ? M - m0 : 32 * MT;
-  const __amdgpu_buffer_rsrc_t cr =
-      __builtin_amdgcn_make_buffer_rsrc(Cout + (size_t)m0 * N, 0, (int)(rows * N * 2), 0x00020000);
+    __syncthreads();
 #pragma unroll
-  for (int j = 0; j < 4 * MT; ++j) {
-    const uint32_t row = wave * 8 * MT + 2 * j + h;
-    const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * kCStride + r * 16);
-    __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * N + n) * 2, 0, kSc1);
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t row = i * 32 + wave * 8 + 2 * j + h;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * kCStride + r * 16);
+      if (n < N) __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * N + n) * 2, 0, kSc1);
+    }
   }
 }
 
