@@ -70,6 +70,7 @@ constexpr int DA = 4;      // A stages are copied DA chunks ahead of use
 constexpr int WD = 4;      // weight register sets (chunks of weight prefetch)
 constexpr int kCStride = kPanelsPerTile * kPanelRows * 2 + 16;  // epilogue tile row pitch
 constexpr uint32_t kMaxSplits = 4;  // split-K workgroups per tile
+constexpr int kSplitTile = 2;       // m-tiles per tile where 128-row tiles would split K
 
 template <int MT>
 struct Geometry {
@@ -264,10 +265,11 @@ __device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, ui
   const uint32_t m0 = lds_addr(slot) + p.a_lds;
   if (s == 0) {
     if constexpr (MT >= 2) dma_group<MT, 0>(wa, p, c, m0);
-    if constexpr (MT >= 4) dma_group<MT, 1>(wa, p, c, m0);
+    if constexpr (MT >= 3) dma_group<MT, 1>(wa, p, c, m0);
   } else if (s == 1) {
     if constexpr (MT == 1) dma_group<MT, 0>(wa, p, c, m0);
     if constexpr (MT == 2) dma_group<MT, 1>(wa, p, c, m0);
+    if constexpr (MT == 3) dma_group<MT, 2>(wa, p, c, m0);
     if constexpr (MT == 4) {
       dma_group<MT, 2>(wa, p, c, m0);
       dma_group<MT, 3>(wa, p, c, m0);
@@ -772,7 +774,7 @@ extern "C" int madi_q8_gemm(const void *a, const void *qs, const void *scales, v
   // count and the partial sums through memory (fc2 at M = 1500: 2 splits of
   // 40 chunks instead of 4 of 20, 35 -> 30.5 us).
   if (split_count(tile_count(m, n, 4), k / kChunkK) > 1)
-    return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k);
+    return dispatch_epi<kSplitTile>(epilogue, A, Q, S, C, bias, m, n, k);
   // Otherwise the lowest tiles whose count still fits one workgroup per CU:
   // a lower tile does less MFMA work per byte loaded (a 32-row tile takes
   // ~0.9x the time of a 64-row one for half the work) but spreads over more
@@ -782,5 +784,6 @@ extern "C" int madi_q8_gemm(const void *a, const void *qs, const void *scales, v
   const uint32_t cus = (uint32_t)cu_count();
   if (tile_count(m, n, 1) <= cus) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k);
   if (tile_count(m, n, 2) <= cus) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k);
+  if (tile_count(m, n, 3) <= cus) return dispatch_epi<3>(epilogue, A, Q, S, C, bias, m, n, k);
   return dispatch_epi<4>(epilogue, A, Q, S, C, bias, m, n, k);
 }

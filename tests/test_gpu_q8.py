@@ -93,6 +93,13 @@ def normwise(c, ref):
     return np.max(np.abs(c - ref)) / max(np.max(np.abs(ref)), 1e-30)
 
 
+def tile_rows(m):
+    """Rows at every 32-row boundary of an m-row GEMM and a random sample."""
+    edges = np.arange(0, m, 32)
+    rows = np.r_[edges, edges - 1, m - 1, np.random.default_rng(m).integers(0, m, 8)]
+    return np.unique(rows[(rows >= 0) & (rows < m)])
+
+
 # ------------------------------------------------------------------ layout
 @pytest.mark.parametrize("n,k", [(64, 128), (100, 256), (51866, 1280)])
 def test_device_repack_matches_host(q, n, k):
@@ -167,18 +174,11 @@ def test_gemm_parity_small(q, m, n, k):
     assert tight_ok(c, a, qs, sc)
 
 
-def tile_rows(m):
-    """Rows at every 32-row boundary of an m-row GEMM and a random sample."""
-    edges = np.arange(0, m, 32)
-    rows = np.r_[edges, edges - 1, m - 1, np.random.default_rng(m).integers(0, m, 8)]
-    return np.unique(rows[(rows >= 0) & (rows < m)])
-
-
 # One shape per m-tile height on a 256-CU device: 32-row tiles (m = 20, and
 # m = 130, where 32-row tiles still fit one workgroup per CU), 64-row tiles
-# (m = 33) and 128-row tiles (m = 520 at n = 8192: 64-row tiles would be 288
-# workgroups).
-TILE_SHAPES = [(20, 320), (33, 320), (130, 320), (520, 8192)]
+# (m = 33), 96-row tiles (m = 700 at n = 8192: 256 tiles, where 64-row tiles
+# would be 352) and 128-row tiles (m = 800: 96-row tiles would be 288).
+TILE_SHAPES = [(20, 320), (33, 320), (130, 320), (700, 8192), (800, 8192)]
 
 
 @pytest.mark.parametrize("k", [128, 256, 320, 512, 768, 1024])
@@ -254,8 +254,7 @@ def test_gemm_encoder_shapes_full_m(q, name, n, k):
     m = 1500
     a, qs, sc = synth.gemm_case(0, m, n, k)
     c = _gemm(q, a, qs, sc)
-    rows = np.unique(np.r_[0, 1, 31, 32, 127, 128, 129, 767, 768, 1407, 1408, 1471, 1472,
-                           1498, 1499, np.random.default_rng(1).integers(0, m, 16)])
+    rows = np.unique(np.r_[tile_rows(m), 1, 129, 1498])  # every 32-row tile boundary
     ref = O.q8_gemm_rows(a, qs, sc, rows=rows, threads=16)
     assert normwise(c[rows], ref) <= TOL
     assert np.all(np.isfinite(c))
