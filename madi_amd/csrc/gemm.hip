@@ -388,29 +388,30 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint3
 }
 
 template <int MT, int EPI, bool PADDED>
-__global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
-                                                      const uint8_t *__restrict__ qs,
-                                                      const f16 *__restrict__ sc,
-                                                      f16 *__restrict__ Cout,
-                                                      const float *__restrict__ bias, uint32_t M,
-                                                      uint32_t N, uint32_t K, uint32_t tiles_m,
-                                                      uint32_t tiles_n, uint32_t group_m,
-                                                      uint32_t splits, float *__restrict__ ws,
-                                                      uint32_t *__restrict__ cnt) {
+__global__ __launch_bounds__(256) void q8_gemm_kernel(
+    const f16 *__restrict__ A, const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
+    uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m, uint32_t tiles_n, uint32_t group_m,
+    uint32_t cper, uint32_t crem, f16 *__restrict__ Cout, const float *__restrict__ bias,
+    float *__restrict__ ws, uint32_t *__restrict__ cnt) {
   using G = Geometry<MT>;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G::kLds];
   __shared__ uint32_t arrived;
 
-  // ---- tile order: consecutive workgroups go to different XCDs (round-robin),
-  // so renumber to give each XCD a contiguous run, then walk that run in
-  // groups of `group_m` M-tiles so an XCD's tiles share A rows and W panels
-  // in its own L2.  With split K, workgroup (split, tile) covers K chunks
-  // [split * C / splits, (split + 1) * C / splits) of tile `tile`.
+  // ---- tile order: consecutive workgroups go to different XCDs (round-robin,
+  // x fastest), so renumber x to give each XCD a contiguous run, then walk
+  // that run in groups of `group_m` M-tiles so an XCD's tiles share A rows
+  // and W panels in its own L2.  The grid's y index is the K split: split s
+  // covers chunks [s * cper + min(s, crem), + cper + (s < crem)) of the
+  // tile.  The arguments the mapping needs come first and arrive preloaded
+  // in SGPRs; C, the bias and the split-K workspace, needed only at the end,
+  // follow.
   const uint32_t T = tiles_m * tiles_n;
-  uint32_t bid = blockIdx.x;
-  if ((T * splits) % 8 == 0) bid = (bid % 8) * (T * splits / 8) + bid / 8;
-  const uint32_t split = bid / T;
-  bid %= T;
+  // (a mask, not a branch: at a branch the compiler copies the kernel
+  // arguments still being loaded, which waits for them)
+  const uint32_t bid_x = blockIdx.x;
+  const uint32_t remap = 0u - (uint32_t)((T & 7) == 0);  // all ones when T % 8 == 0
+  const uint32_t bid = (((bid_x & 7) * (T >> 3) + (bid_x >> 3)) & remap) | (bid_x & ~remap);
+  const uint32_t split = blockIdx.y, splits = gridDim.y;
   const uint32_t tile = bid;
   const uint32_t per_group = group_m * tiles_n;
   const uint32_t gi = bid / per_group, first_m = gi * group_m;
@@ -422,8 +423,9 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(const f16 *__restrict__ A,
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
   const uint32_t m0 = tm * 32 * MT, p0 = tn * kPanelsPerTile;
-  const uint32_t np = N / kPanelRows, call = K / kChunkK;
-  const uint32_t cb = split * call / splits, nchunks = (split + 1) * call / splits - cb;
+  const uint32_t np = N / kPanelRows;
+  const uint32_t cb = split * cper + (split < crem ? split : crem);
+  const uint32_t nchunks = cper + (split < crem ? 1 : 0);
 
   // ---- load plan.  Panels past N and rows past M are clamped to the last
   // valid one: their bytes are read but their results are never stored.
@@ -715,21 +717,22 @@ int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const fl
     const int rc = workspace(part, T, &ws, &cnt);
     if (rc != MADI_OK) return rc;
   }
-  // every split's chunk count a multiple of WD and at least 2*WD: the
-  // select-free loop
+  // split s covers cper + (s < crem) chunks; every split's chunk count a
+  // multiple of WD and at least 2*WD: the select-free loop
+  const uint32_t cper = chunks / splits, crem = chunks % splits;
   bool padded = false;
-  for (uint32_t s = 0; s < splits; ++s) {
-    const uint32_t n = (s + 1) * chunks / splits - s * chunks / splits;
+  for (const uint32_t n : {cper, cper + 1}) {
+    if (n == cper + 1 && crem == 0) continue;
     if (n % WD || n < 2 * WD) padded = true;
   }
   if (padded)
-    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, true>), dim3(T * splits), dim3(kWaves * 64), 0,
-                       stream(), A, qs, sc, C, bias, M, N, K, tiles_m, tiles_n, group_m, splits,
-                       ws, cnt);
+    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, true>), dim3(T, splits), dim3(kWaves * 64), 0,
+                       stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
+                       bias, ws, cnt);
   else
-    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false>), dim3(T * splits), dim3(kWaves * 64), 0,
-                       stream(), A, qs, sc, C, bias, M, N, K, tiles_m, tiles_n, group_m, splits,
-                       ws, cnt);
+    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false>), dim3(T, splits), dim3(kWaves * 64), 0,
+                       stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
+                       bias, ws, cnt);
   return check_launch("madi_q8_gemm");
 }
 
