@@ -430,6 +430,8 @@ def staged_ok(c, x, qs, sc):
     (1, 3840, 1280), (2, 3840, 1280), (8, 5120, 1280), (16, 1280, 5120),
     (8, 51866, 1280),    # batched vocab logits, tail panel of 26 rows
     (32, 1280, 1280), (33, 3840, 1280), (70, 1280, 5120), (5, 40, 64),
+    (17, 5120, 1280),    # one 32-row slice, 15 rows past M
+    (320, 1280, 1280),   # sequence prefill at its largest M: ten slices
 ])
 def test_pproj_parity(q, m, n, k):
     say(f"pproj m={m} n={n} k={k}")
