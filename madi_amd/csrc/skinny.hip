@@ -339,6 +339,9 @@ extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const 
   // (32*k*4 bytes) must stay below 2 GiB
   if ((uint64_t)n * k >= (1ull << 31) || (uint64_t)kSlice * k * 4 >= (1ull << 31))
     return fail(MADI_ERR_SHAPE, "madi_q8_pproj: n=%u k=%u exceeds the 2 GiB operand limit", n, k);
+  // the 32-row activation slices are the grid's y extent
+  if ((m + kSlice - 1) / kSlice > 65535)
+    return fail(MADI_ERR_SHAPE, "madi_q8_pproj: m=%u exceeds %u rows", m, 65535u * kSlice);
   if (!aligned(qs, 16) || !aligned(scales, 2) || !aligned(in, 16) || !aligned(out, 4))
     return fail(MADI_ERR_ALIGN, "madi_q8_pproj: qs and in need 16-byte alignment");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_pproj: madi_init has not succeeded");

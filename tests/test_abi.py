@@ -66,6 +66,11 @@ FAKE = 0x100000  # 16-byte aligned, never dereferenced: every call below fails v
     ("madi_q8_repack", (FAKE, FAKE + 4096, FAKE, FAKE + 8192, 32, 64), -9),        # overlap
     ("madi_q8_emb_lookup", (FAKE, FAKE, FAKE, FAKE, 51866, 1000), -5),
     ("madi_q8_emb_lookup", (FAKE, FAKE, FAKE, None, 51866, 1280), -6),
+    ("madi_q8_pproj", (FAKE, FAKE, FAKE, FAKE, 0, 1280, 1280), -5),               # m == 0
+    ("madi_q8_pproj", (FAKE, FAKE, FAKE, FAKE, 65535 * 32 + 1, 32, 64), -5),      # slices > grid y
+    ("madi_q8_pproj", (FAKE, None, FAKE, FAKE, 8, 1280, 1280), -6),
+    ("madi_q8_pproj", (FAKE, FAKE + 4, FAKE, FAKE, 8, 1280, 1280), -7),
+    ("madi_q8_pproj", (FAKE, FAKE, FAKE, FAKE, 65535 * 32, 32, 64), -8),         # largest M, not initialised
     ("madi_alloc", (16,), None),
     ("madi_sync", (), -8),
     ("madi_upload", (FAKE, FAKE, 16), -8),
