@@ -2,16 +2,17 @@
 //
 // Replaces gemv_q8 / _bias / _bias_gelu / _bias_res / _qkv and logit_gemv_q8
 // (engine/metal/kernels/graph_helpers.metal:320-558).  The reference runs one
-// 32-lane simdgroup per output row reading char4 + float4; here a 256-thread
-// workgroup owns one 32-row panel of the panel layout and its four waves split
-// K (sixteen waves for the decoder's 40 - 160-panel matrices, so that a
-// K = 1280 range is one round of loads).  Every wave64 load instruction moves one contiguous KiB (16 bytes per
-// lane, lane (h, r) receiving 16 weights of row r in quantisation block h),
-// issued as a buffer load with the panel/chunk offset in an SGPR.  Each wave
-// streams its K range through a two-chunk window (use chunk c, refill with
-// chunk c+2).  The kernel keeps to 72 VGPRs (seven waves per SIMD, seven
-// workgroups per CU), so every workgroup of the 51866-row vocab matrix (1621
-// panels) is resident from the start.
+// 32-lane simdgroup per output row reading char4 + float4; here a workgroup
+// owns one 32-row panel of the panel layout and its waves split K: four for
+// the vocab matrix, sixteen for the decoder's 40 - 160-panel matrices (so a
+// K = 1280 range is one round of loads).  Every wave64 load instruction moves
+// one contiguous KiB (16 bytes per lane, lane (h, r) receiving 16 weights of
+// row r in quantisation block h), issued as a buffer load with the
+// panel/chunk offset in an SGPR.  Each wave streams its K range through a
+// two-chunk window (use chunk c, refill with chunk c+2).  The kernel keeps to
+// 48 - 65 VGPRs (seven waves per SIMD), so every four-wave workgroup of the
+// 51866-row vocab matrix (1621 panels, seven per CU) is resident from the
+// start.
 //
 // The activation vector is loaded before the weights, staged once per
 // workgroup in LDS and read back as broadcast 128-bit LDS loads.  v_perm_b32
