@@ -101,25 +101,24 @@ __device__ inline float gelu_erf(float xv) {
 }
 
 // The same erf-form GELU in fewer instructions, for epilogues that apply it
-// to every element of a tile (128 values per lane in the GEMM): the hardware
-// reciprocal (1 ulp) for 1 / (1 + p|z|), the hardware exp2 (its argument is
-// clamped to >= -80, so the result is a normal number), and fused final
-// steps.  Differs from gelu_erf by a few fp32 ulps, far inside one rounding
-// of the f16 result.
+// to every element of a tile (128 values per lane in the GEMM): with
+// z = x / sqrt(2), 1 / (1 + p|z|) takes p / sqrt(2) against |x| (one FMA and
+// the hardware reciprocal, 1 ulp), e^(-z^2) is the hardware exp2 of
+// (x * -log2(e) / 2) * x (it returns 0 where that underflows, where
+// erf(|z|) is 1 in fp32 anyway), and x/2 (1 + sign(x) erf(|z|)) is
+// x/2 + |x/2| erf(|z|), one FMA.  Differs from gelu_erf by a few fp32 ulps,
+// far inside one rounding of the f16 result.
 __device__ inline float gelu_erf_fast(float xv) {
-  const float z = xv * 0.7071067811865476f;
-  const float az = __builtin_fabsf(z);
-  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(az, 0.3275911f, 1.0f));
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(__builtin_fabsf(xv), 0.23164189f, 1.0f));
   float poly = __builtin_fmaf(1.061405429f, t, -1.453152027f);
   poly = __builtin_fmaf(poly, t, 1.421413741f);
   poly = __builtin_fmaf(poly, t, -0.284496736f);
   poly = __builtin_fmaf(poly, t, 0.254829592f);
   poly = poly * t;
-  const float ex =
-      __builtin_amdgcn_exp2f(__builtin_fmaxf(-az * az * 1.4426950408889634f, -80.0f));
-  const float erf = __builtin_copysignf(__builtin_fmaf(-poly, ex, 1.0f), z);
+  const float ex = __builtin_amdgcn_exp2f((xv * -0.72134752044448170f) * xv);
+  const float erf_abs = __builtin_fmaf(-poly, ex, 1.0f);  // erf(|z|)
   const float hx = 0.5f * xv;
-  return __builtin_fmaf(hx, erf, hx);
+  return __builtin_fmaf(__builtin_fabsf(hx), erf_abs, hx);
 }
 
 }  // namespace madi
