@@ -218,6 +218,21 @@ def test_gemm_split_k(q, m, n, k):
         assert tight_ok(c, a, qs, sc)
 
 
+def test_gemm_gelu_tails(q):
+    """bias + GELU where the pre-activation spans +-40: the far negative tail
+    must come out as (signed) zero and the positive tail as v itself, where
+    e^(-z^2) underflows (fp32 exp2 below its range) and erf(|z|) is 1."""
+    m, n, k = 33, 512, 128
+    say(f"gemm gelu tails m={m} n={n} k={k}")
+    a, qs, sc = synth.gemm_case(41, m, n, k)
+    a = (a.astype(np.float32) * 0.01).astype(np.float16)
+    bias = np.linspace(-40.0, 40.0, n).astype(np.float32)
+    c = _gemm(q, a, qs, sc, bias=bias, gelu=True)
+    assert np.all(np.isfinite(c))
+    assert tight_epi_ok(c, a, qs, sc, bias, True)
+    assert np.all(np.abs(c[:, :16].astype(np.float32)) < 1e-6)  # v < -37: GELU(v) ~ -1e-300
+
+
 def test_gemm_one_hot_is_dequant(q):
     """A = identity rows: each output row is one dequantised weight column,
     bit-exact (one exact product, fp32 sum of zeros, exact f16 store)."""
