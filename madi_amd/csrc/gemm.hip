@@ -48,15 +48,20 @@
 // touching memory, so they add exact zeros.  Loads are issued in the same
 // pattern every chunk, which keeps every vmcnt wait a constant.
 //
+// Tile height: 32, 64, 96 or 128 rows (MT = 1..4), chosen per shape by the
+// host so the tile count fills the CUs in one round where it can.
+//
 // Split K: when the tiles alone cannot fill the GPU and K is long (fc2,
-// 5120 -> 1280 at M = 1500, makes 60 tiles), up to four workgroups share a
-// tile, each over a contiguous K range.  Each publishes its fp32 partial tile
-// to the library's workspace and counts itself in with a system-scope atomic;
-// the last to arrive adds the other partials and runs the epilogue.
+// 5120 -> 1280 at M = 1500: 120 tiles of 64 rows), up to four workgroups
+// share a tile, each over a contiguous K range (the grid's y index).  Each
+// publishes its fp32 partial tile to the library's workspace and counts
+// itself in with a system-scope atomic; the last to arrive adds the partials
+// in split order and runs the epilogue.
 //
 // Epilogue: bias / GELU in fp32 registers, one rounding to f16, then the tile
-// is transposed through LDS so every global store writes whole 512-byte row
-// segments (16 bytes per lane).
+// leaves through LDS one 32-row m-tile at a time (the stores of one m-tile
+// overlap the conversion of the next), transposed so every global store
+// writes whole 512-byte row segments (16 bytes per lane).
 #include "common.h"
 
 using namespace madi;
