@@ -388,7 +388,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip the encoder-window, batched-decode and long-audio measurements")
+                    help="skip the encoder-window, batched-decode, decoder-token and long-audio "
+                         "measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (PMC calibration)")
     args = ap.parse_args()
