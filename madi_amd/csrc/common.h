@@ -19,7 +19,9 @@ hipStream_t stream();
 int cu_count();
 // The library's split-K workspace: `partial_bytes` of fp32 partial sums and
 // `counters` arrival counters that are zero whenever no kernel is using them.
-// Grows on demand (a grow waits for the device); freed by madi_cleanup.
+// Grows on demand (a grow waits for the device; an outgrown buffer is kept,
+// not freed, because graphs captured earlier still name it); all of them are
+// freed by madi_cleanup.
 int workspace(size_t partial_bytes, size_t counters, float **partials, uint32_t **cnt);
 // Releases the fp16 GEMM's rocBLAS handle (madi_cleanup).
 void f16gemm_cleanup();

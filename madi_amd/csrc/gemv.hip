@@ -299,6 +299,10 @@ int launch(const char *what, const GemvArgs &a) {
   if (a.n == 0 || a.k == 0 || a.k % kChunkK)
     return fail(MADI_ERR_SHAPE, "%s: n=%u k=%u (need n > 0, k a positive multiple of 64)", what, a.n, a.k);
   if (a.k > kMaxK) return fail(MADI_ERR_SHAPE, "%s: k=%u exceeds %u", what, a.k, kMaxK);
+  // buffer ranges and offsets are 32-bit: the weight (n*k bytes) must stay
+  // below 2 GiB, as for the GEMM and the batched projection
+  if ((uint64_t)a.n * a.k >= (1ull << 31))
+    return fail(MADI_ERR_SHAPE, "%s: n=%u k=%u exceeds the 2 GiB operand limit", what, a.n, a.k);
   if (!aligned(a.qs, 16) || !aligned(a.sc, 2) || !aligned(a.x, 16))
     return fail(MADI_ERR_ALIGN, "%s: qs and x need 16-byte alignment", what);
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);

@@ -20,12 +20,20 @@ hipStream_t g_stream = nullptr;
 constexpr size_t kCounters = 16384;
 void *g_ws = nullptr;
 size_t g_ws_bytes = 0;
+// Workspaces outgrown by a larger split shape.  A HIP graph captured before
+// the growth still names the old buffer in its kernel arguments, so an
+// outgrown buffer stays allocated (and its counters at zero) until
+// madi_cleanup; freeing it would let a replay write partial sums into
+// memory that may have been handed out again.
+constexpr int kMaxRetired = 32;
+void *g_retired[kMaxRetired];
+int g_nretired = 0;
 
 void free_workspace() {
-  if (g_ws) {
-    (void)hipDeviceSynchronize();
-    (void)hipFree(g_ws);
-  }
+  if (g_ws || g_nretired) (void)hipDeviceSynchronize();
+  if (g_ws) (void)hipFree(g_ws);
+  for (int i = 0; i < g_nretired; ++i) (void)hipFree(g_retired[i]);
+  g_nretired = 0;
   g_ws = nullptr;
   g_ws_bytes = 0;
 }
@@ -43,21 +51,26 @@ int workspace(size_t partial_bytes, size_t counters, float **partials, uint32_t 
       return fail(MADI_ERR_ARG,
                   "split-K workspace must grow to %zu bytes, which cannot happen during graph "
                   "capture; run this GEMM shape once before capturing", need);
-    // kernels still running may hold the old buffer: free_workspace waits for them
-    free_workspace();
-    hipError_t e = hipMalloc(&g_ws, need);
-    if (e != hipSuccess) {
-      g_ws = nullptr;
-      return fail(MADI_ERR_ALLOC, "split-K workspace (%zu bytes): %s", need, hipGetErrorString(e));
-    }
+    // the old buffer is retired, not freed (kernels still running and graphs
+    // captured earlier may use it); growing at least twofold keeps the
+    // number of retired buffers logarithmic in the largest shape
+    if (g_ws && g_nretired == kMaxRetired)
+      return fail(MADI_ERR_ALLOC, "split-K workspace: %d growths already retired", kMaxRetired);
+    const size_t grow = g_ws_bytes * 2 > need ? g_ws_bytes * 2 : need;
+    void *fresh = nullptr;
+    hipError_t e = hipMalloc(&fresh, grow);
+    if (e != hipSuccess)
+      return fail(MADI_ERR_ALLOC, "split-K workspace (%zu bytes): %s", grow, hipGetErrorString(e));
     // the counters start at zero; every use returns them to zero
-    e = hipMemset(g_ws, 0, kCounters * 4);
+    e = hipMemset(fresh, 0, kCounters * 4);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
-      free_workspace();
+      (void)hipFree(fresh);
       return fail(MADI_ERR_ALLOC, "split-K workspace: clearing the counters: %s", hipGetErrorString(e));
     }
-    g_ws_bytes = need;
+    if (g_ws) g_retired[g_nretired++] = g_ws;
+    g_ws = fresh;
+    g_ws_bytes = grow;
   }
   *cnt = static_cast<uint32_t *>(g_ws);
   *partials = reinterpret_cast<float *>(static_cast<uint8_t *>(g_ws) + kCounters * 4);

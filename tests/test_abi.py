@@ -55,6 +55,8 @@ FAKE = 0x100000  # 16-byte aligned, never dereferenced: every call below fails v
     ("madi_q8_gemm", (FAKE, FAKE, FAKE, FAKE, None, 16, 256, 1280, 0), -8),       # not initialised
     ("madi_q8_gemv", (FAKE, FAKE, FAKE, FAKE, 100, 96), -5),
     ("madi_q8_gemv", (FAKE, FAKE, FAKE + 8, FAKE, 100, 1280), -7),
+    ("madi_q8_gemv", (FAKE, FAKE, FAKE, FAKE, 1 << 21, 1024), -5),                # 2 GiB weight
+    ("madi_q8_logit_gemv", (FAKE, FAKE, FAKE, FAKE, 1 << 22, 512), -5),           # 2 GiB vocab
     ("madi_q8_gemv", (FAKE, FAKE, FAKE, FAKE, 100, 1280), -8),
     ("madi_q8_gemv_bias", (FAKE, FAKE, FAKE, FAKE, None, 100, 1280), -6),
     ("madi_q8_gemv_qkv", (FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, None, 1280), -6),

@@ -519,6 +519,62 @@ def test_graph_replay_decode_sequence(q):
         q.sync()
 
 
+def test_graph_replay_after_workspace_growth(q):
+    """Split-K launches captured while the workspace holds its initial 4 MiB
+    (a fresh library: madi_cleanup then madi_init), then an eager split GEMM
+    that needs 15.7 MB grows it: the outgrown buffer stays allocated, so the
+    graph's kernels, which still name it, replay to the eager results."""
+    say("graph replay after workspace growth")
+    from madi_amd import _lib
+    _lib.lib().madi_cleanup()
+    q.init()
+    rng = np.random.default_rng(37)
+    qs1, sc1 = synth.q8_weight(rng, 1280, 5120)     # FFN down: four K splits
+    w1 = q.upload_q8(qs1, sc1)
+    x = dev(rng.standard_normal((8, 5120)).astype(np.float32))
+    xv = dev(rng.standard_normal(5120).astype(np.float32))
+    a = dev_f16(synth.activations(rng, 20, 4096))
+    qs2, sc2 = synth.q8_weight(rng, 512, 4096)      # 2 tiles x 4 K splits
+    w2 = q.upload_q8(qs2, sc2)
+    o1 = torch.empty((8, 1280), dtype=torch.float32, device="cuda")
+    o2 = torch.empty(1280, dtype=torch.float32, device="cuda")
+    c = torch.empty((20, 512), dtype=torch.int16, device="cuda")
+
+    def seq():
+        q.pproj(x, w1, o1, 8, 1280, 5120)
+        q.kGemvQ8(o2, xv, w1, 1280, 5120)
+        q.kGemmQ8(a, w2, c, 20, 512, 4096)
+
+    seq()
+    q.sync()
+    want = (o1.clone(), o2.clone(), c.clone())
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            q.init(side)
+            seq()
+    q.init()
+    # fc2 at M = 1500 (two splits of 120 tiles) grows the workspace past 4 MiB
+    a3, qs3, sc3 = synth.gemm_case(38, 1500, 1280, 5120)
+    w3 = q.upload_q8(qs3, sc3)
+    c3 = torch.empty((1500, 1280), dtype=torch.int16, device="cuda")
+    q.kGemmQ8(dev_f16(a3), w3, c3, 1500, 1280, 5120)
+    q.sync()
+    rows = tile_rows(1500)
+    assert normwise(host_f16(c3)[rows], O.q8_gemm_rows(a3, qs3, sc3, rows=rows, threads=8)) <= TOL
+    for rep in range(3):
+        for t in (o1, o2):
+            t.fill_(float("nan"))
+        c.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o1, want[0]) and torch.equal(o2, want[1]) and torch.equal(c, want[2]), rep
+        seq()
+        q.sync()
+
+
 # ------------------------------------------------------------------ load path: quantise, Q8 files
 def _knife_edge_weights(rng, n, k):
     """Random f16 rows plus planted blocks: all zero (scale 1.0), exact half
