@@ -140,6 +140,21 @@ int madi_q8_dequant_f16(void *wdq, const void *qs, const void *scales, uint32_t 
 int madi_q8_gemm(const void *a, const void *qs, const void *scales, void *c,
                  const float *bias, uint32_t m, uint32_t n, uint32_t k, int epilogue);
 
+/* No counterpart in the reference: madi_q8_gemm for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * madi_q8_gemm, bit for bit; where a shape splits K over workgroups, the
+ * partial sums and arrival counters live in a fixed 16 MiB device array of
+ * the library (MADI_Q8_GEMM_NOALLOC_SCRATCH bytes per GPU, held until the
+ * process ends) instead of the growable workspace, so the call allocates
+ * nothing.  Every split shape of madi_q8_gemm fits (at most 15 MiB of
+ * partials); a larger need fails with MADI_ERR_SHAPE.  All calls on one GPU
+ * share that GPU's array: calls that overlap on one GPU (several streams or
+ * host threads) race and must not. */
+#define MADI_Q8_GEMM_NOALLOC_SCRATCH (16u << 20)
+int madi_q8_gemm_noalloc(const void *a, const void *qs, const void *scales, void *c,
+                         const float *bias, uint32_t m, uint32_t n, uint32_t k, int epilogue);
+
 /* Decoder GEMVs, x f32 [K] -> out f32 [N] (M = 1).  Argument order of the Zig
  * wrappers (engine/metal/decoder.zig:155-181) with the Q8w struct spelled out as
  * (qs, scales):

@@ -46,6 +46,7 @@ SIGNATURES = {
     "madi_q8_fnv": (ctypes.c_uint64, [ctypes.c_uint64, _P, _SZ, _P, _SZ]),
     "madi_q8_dequant_f16": (_I, [_P, _P, _P, _U32, _U32]),
     "madi_q8_gemm": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _I]),
+    "madi_q8_gemm_noalloc": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _I]),
     "madi_q8_gemv": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_gemv_bias": (_I, [_P, _P, _P, _P, _P, _U32, _U32]),
     "madi_q8_gemv_bias_gelu": (_I, [_P, _P, _P, _P, _P, _U32, _U32]),

@@ -25,6 +25,9 @@ int cu_count();
 int workspace(size_t partial_bytes, size_t counters, float **partials, uint32_t **cnt);
 // Releases the fp16 GEMM's rocBLAS handle (madi_cleanup).
 void f16gemm_cleanup();
+// Resolves the current device's address of the allocation-free GEMM's fixed
+// scratch array and clears its counters (madi_init).
+int gemm_scratch_init();
 
 inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 

@@ -707,9 +707,58 @@ uint32_t tile_count(uint32_t M, uint32_t N, uint32_t MT) {
   return (M + 32 * MT - 1) / (32 * MT) * ((N + 255) / 256);
 }
 
+// ---- fixed scratch for the allocation-free entry point.  A K split's
+// partial sums and arrival counters live in this device array instead of
+// the library's growable workspace: kScratchCounters counters (zero whenever
+// no kernel is using them: every split tile's last workgroup resets its
+// own), then the partials.  A split happens only below 160 tiles and only at
+// 32- or 64-row tiles, and splits * tiles <= 240, so the partials of any
+// split shape take at most 240 * 64 KiB = 15 MiB.
+constexpr size_t kScratchBytes = size_t(16) << 20;
+constexpr size_t kScratchCounters = 1024;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Device address of `scratch` per device.  In host code the array's name is
+// only a host-side stand-in, so the kernels take this address instead,
+// resolved with hipGetSymbolAddress once per device, with that device current.
+constexpr int kMaxDevices = 64;
+uint8_t *g_scratch[kMaxDevices];
+
+__global__ void zero_counters_kernel(uint32_t *cnt, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) cnt[i] = 0;
+}
+
+// Resolves the current device's scratch address (once) and clears its
+// counters.  Runs in madi_init, before any caller can be capturing a graph.
+int resolve_scratch(uint8_t **out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MADI_ERR_INIT, "scratch: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MADI_ERR_INIT, "scratch: device %d out of range", dev);
+  if (!g_scratch[dev]) {
+    void *ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(MADI_ERR_INIT, "scratch: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    hipLaunchKernelGGL(zero_counters_kernel, dim3(kScratchCounters / 256), dim3(256), 0, nullptr,
+                       static_cast<uint32_t *>(ptr), (uint32_t)kScratchCounters);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess)
+      return fail(MADI_ERR_INIT, "scratch: clearing the counters: %s", hipGetErrorString(e));
+    g_scratch[dev] = static_cast<uint8_t *>(ptr);
+  }
+  *out = g_scratch[dev];
+  return MADI_OK;
+}
+
+// Where a launch keeps its split-K partials and counters.
+enum Scratch { kWorkspace = 0, kStatic = 1 };
+
 template <int MT, int EPI>
 int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const float *bias,
-                uint32_t M, uint32_t N, uint32_t K) {
+                uint32_t M, uint32_t N, uint32_t K, Scratch where) {
   const uint32_t tiles_m = (M + 32 * MT - 1) / (32 * MT);
   const uint32_t tiles_n = (N + 255) / 256;
   const uint32_t group_m = tiles_m < 6 ? tiles_m : 6;
@@ -719,8 +768,20 @@ int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const fl
   uint32_t *cnt = nullptr;
   if (splits > 1) {
     const size_t part = (size_t)T * splits * (4 * 2 * MT * 4 * 64 * 16);
-    const int rc = workspace(part, T, &ws, &cnt);
-    if (rc != MADI_OK) return rc;
+    if (where == kStatic) {
+      if (T > kScratchCounters || part > kScratchBytes - kScratchCounters * 4)
+        return fail(MADI_ERR_SHAPE,
+                    "madi_q8_gemm_noalloc: m=%u n=%u k=%u needs %zu bytes of split-K scratch, "
+                    "more than the %zu the library holds", M, N, K,
+                    part + kScratchCounters * 4, kScratchBytes);
+      uint8_t *base = nullptr;
+      if (int rc = resolve_scratch(&base)) return rc;
+      cnt = reinterpret_cast<uint32_t *>(base);
+      ws = reinterpret_cast<float *>(base + kScratchCounters * 4);
+    } else {
+      const int rc = workspace(part, T, &ws, &cnt);
+      if (rc != MADI_OK) return rc;
+    }
   }
   // split s covers cper + (s < crem) chunks; every split's chunk count a
   // multiple of WD and at least 2*WD: the select-free loop
@@ -743,46 +804,45 @@ int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const fl
 
 template <int MT>
 int dispatch_epi(int epi, const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C,
-                 const float *bias, uint32_t M, uint32_t N, uint32_t K) {
+                 const float *bias, uint32_t M, uint32_t N, uint32_t K, Scratch where) {
   switch (epi) {
-  case MADI_EPI_NONE: return launch_gemm<MT, MADI_EPI_NONE>(A, qs, sc, C, bias, M, N, K);
-  case MADI_EPI_BIAS: return launch_gemm<MT, MADI_EPI_BIAS>(A, qs, sc, C, bias, M, N, K);
-  case MADI_EPI_BIAS_GELU: return launch_gemm<MT, MADI_EPI_BIAS_GELU>(A, qs, sc, C, bias, M, N, K);
+  case MADI_EPI_NONE: return launch_gemm<MT, MADI_EPI_NONE>(A, qs, sc, C, bias, M, N, K, where);
+  case MADI_EPI_BIAS: return launch_gemm<MT, MADI_EPI_BIAS>(A, qs, sc, C, bias, M, N, K, where);
+  case MADI_EPI_BIAS_GELU:
+    return launch_gemm<MT, MADI_EPI_BIAS_GELU>(A, qs, sc, C, bias, M, N, K, where);
   default: return fail(MADI_ERR_ARG, "madi_q8_gemm: unknown epilogue %d", epi);
   }
 }
 
-}  // namespace
-
-extern "C" int madi_q8_gemm(const void *a, const void *qs, const void *scales, void *c,
-                            const float *bias, uint32_t m, uint32_t n, uint32_t k, int epilogue) {
-  if (!a || !qs || !scales || !c) return fail(MADI_ERR_NULL, "madi_q8_gemm: null pointer");
-  if (epilogue != MADI_EPI_NONE && !bias) return fail(MADI_ERR_NULL, "madi_q8_gemm: null bias");
+int q8_gemm(const char *what, const void *a, const void *qs, const void *scales, void *c,
+            const float *bias, uint32_t m, uint32_t n, uint32_t k, int epilogue, Scratch where) {
+  if (!a || !qs || !scales || !c) return fail(MADI_ERR_NULL, "%s: null pointer", what);
+  if (epilogue != MADI_EPI_NONE && !bias) return fail(MADI_ERR_NULL, "%s: null bias", what);
   if (epilogue == MADI_EPI_BIAS_RES)
-    return fail(MADI_ERR_ARG, "madi_q8_gemm: the residual epilogue exists for the GEMV only");
+    return fail(MADI_ERR_ARG, "%s: the residual epilogue exists for the GEMV only", what);
   if (m == 0 || n == 0 || k == 0 || n % kPanelRows || k % kChunkK)
-    return fail(MADI_ERR_SHAPE, "madi_q8_gemm: m=%u n=%u k=%u (need n %% 32 == 0, k %% 64 == 0)", m, n, k);
+    return fail(MADI_ERR_SHAPE, "%s: m=%u n=%u k=%u (need n %% 32 == 0, k %% 64 == 0)", what, m, n, k);
   // buffer offsets are 32-bit (and buffer sizes below 2 GiB): the operands
   // A (m*k*2 bytes) and W (n*k bytes) and one 128-row C tile (256*n bytes)
   // must stay below 2 GiB
   if ((uint64_t)m * k * 2 >= (1ull << 31) || (uint64_t)n * k >= (1ull << 31) ||
       (uint64_t)n * 256 >= (1ull << 31))
-    return fail(MADI_ERR_SHAPE, "madi_q8_gemm: m=%u n=%u k=%u exceeds the 2 GiB operand limit", m, n, k);
+    return fail(MADI_ERR_SHAPE, "%s: m=%u n=%u k=%u exceeds the 2 GiB operand limit", what, m, n, k);
   if (!aligned(a, 16) || !aligned(qs, 16) || !aligned(scales, 16) || !aligned(c, 16) ||
       (bias && !aligned(bias, 16)))
-    return fail(MADI_ERR_ALIGN, "madi_q8_gemm: a/qs/scales/c/bias need 16-byte alignment");
-  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_gemm: madi_init has not succeeded");
+    return fail(MADI_ERR_ALIGN, "%s: a/qs/scales/c/bias need 16-byte alignment", what);
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);
   const f16 *A = static_cast<const f16 *>(a);
   const uint8_t *Q = static_cast<const uint8_t *>(qs);
   const f16 *S = static_cast<const f16 *>(scales);
   f16 *C = static_cast<f16 *>(c);
-  if (m <= 32) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k);
-  if (m <= 64) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k);
+  if (m <= 32) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  if (m <= 64) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k, where);
   // Where 128-row tiles would split K: 64-row tiles, which halve the split
   // count and the partial sums through memory (fc2 at M = 1500: 2 splits of
   // 40 chunks instead of 4 of 20, 35 -> 30.5 us).
   if (split_count(tile_count(m, n, 4), k / kChunkK) > 1)
-    return dispatch_epi<kSplitTile>(epilogue, A, Q, S, C, bias, m, n, k);
+    return dispatch_epi<kSplitTile>(epilogue, A, Q, S, C, bias, m, n, k, where);
   // Otherwise the lowest tiles whose count still fits one workgroup per CU:
   // a lower tile does less MFMA work per byte loaded (a 32-row tile takes
   // ~0.9x the time of a 64-row one for half the work) but spreads over more
@@ -790,8 +850,29 @@ extern "C" int madi_q8_gemm(const void *a, const void *qs, const void *scales, v
   // cross K,V 1280->2560 120 -> 240 tiles (18.2 -> 13.9 us); q,k,v
   // 1280->3840 (180 tiles) and fc1 (240) keep 128 rows.
   const uint32_t cus = (uint32_t)cu_count();
-  if (tile_count(m, n, 1) <= cus) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k);
-  if (tile_count(m, n, 2) <= cus) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k);
-  if (tile_count(m, n, 3) <= cus) return dispatch_epi<3>(epilogue, A, Q, S, C, bias, m, n, k);
-  return dispatch_epi<4>(epilogue, A, Q, S, C, bias, m, n, k);
+  if (tile_count(m, n, 1) <= cus) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  if (tile_count(m, n, 2) <= cus) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  if (tile_count(m, n, 3) <= cus) return dispatch_epi<3>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  return dispatch_epi<4>(epilogue, A, Q, S, C, bias, m, n, k, where);
+}
+
+}  // namespace
+
+namespace madi {
+// madi_init: the current device's scratch address, resolved at set-up.
+int gemm_scratch_init() {
+  uint8_t *base = nullptr;
+  return resolve_scratch(&base);
+}
+}  // namespace madi
+
+extern "C" int madi_q8_gemm(const void *a, const void *qs, const void *scales, void *c,
+                            const float *bias, uint32_t m, uint32_t n, uint32_t k, int epilogue) {
+  return q8_gemm("madi_q8_gemm", a, qs, scales, c, bias, m, n, k, epilogue, kWorkspace);
+}
+
+extern "C" int madi_q8_gemm_noalloc(const void *a, const void *qs, const void *scales, void *c,
+                                    const float *bias, uint32_t m, uint32_t n, uint32_t k,
+                                    int epilogue) {
+  return q8_gemm("madi_q8_gemm_noalloc", a, qs, scales, c, bias, m, n, k, epilogue, kStatic);
 }

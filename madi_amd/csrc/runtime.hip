@@ -125,6 +125,11 @@ extern "C" int madi_init(void) {
     g_init = false;
     return rc;
   }
+  // the allocation-free GEMM's scratch address on this device
+  if (int rc = gemm_scratch_init()) {
+    g_init = false;
+    return rc;
+  }
   g_err[0] = 0;
   return MADI_OK;
 }

@@ -1,0 +1,117 @@
+"""The allocation-free GEMM entry point (madi_q8_gemm_noalloc) against
+madi_q8_gemm through the C ABI: the same kernels, so the results must agree
+bit for bit, on two calls in a row (the second smaller, so it runs on what
+the first left in the fixed scratch array), and under HIP graph capture,
+where the workspace-backed entry point could not grow its buffer."""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from madi_amd import _lib, synth
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def q():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import madi_amd.q8 as q8
+    q8.init()
+    return q8
+
+
+def dev_f16(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float16).view(np.int16)).cuda()
+
+
+def run(q, name, a_d, w, bias_d, m, n, k, epi):
+    c = torch.full((m, n), -1, dtype=torch.int16, device="cuda")
+    _lib.call(name, a_d.data_ptr(), w.qs, w.scales, c.data_ptr(),
+              None if bias_d is None else bias_d.data_ptr(), m, n, k, epi)
+    q.sync()
+    return c.cpu().numpy()
+
+
+# (m, n, k, epilogue): fc2 + bias at M = 1500 (120 tiles of 64 rows, two K
+# splits: 15 MiB of partials), then smaller split shapes (four splits over 45
+# and 2 tiles), then a shape that does not split at all
+CASES = [(1500, 1280, 5120, _lib.EPI_BIAS), (257, 1280, 5120, _lib.EPI_NONE),
+         (20, 512, 4096, _lib.EPI_BIAS_GELU), (96, 512, 1280, _lib.EPI_BIAS_GELU)]
+
+
+def test_noalloc_matches_gemm_two_calls(q):
+    rng = np.random.default_rng(7)
+    for i, (m, n, k, epi) in enumerate(CASES):
+        say(f"noalloc call {i}: m={m} n={n} k={k} epi={epi}")
+        a, qs, sc = synth.gemm_case(100 + i, m, n, k)
+        bias = rng.standard_normal(n).astype(np.float32)
+        w = q.upload_q8(qs, sc)
+        a_d = dev_f16(a)
+        b_d = torch.from_numpy(bias).cuda() if epi != _lib.EPI_NONE else None
+        got = run(q, "madi_q8_gemm_noalloc", a_d, w, b_d, m, n, k, epi)
+        want = run(q, "madi_q8_gemm", a_d, w, b_d, m, n, k, epi)
+        assert np.array_equal(got, want), (m, n, k, epi)
+        rows = np.unique(np.r_[0, 31, 32, 63, 64, m // 2, m - 1])
+        rows = rows[rows < m]
+        ref = O.q8_gemm_rows(a, qs, sc, rows=rows, bias=bias if epi else None,
+                             epilogue=epi, threads=8)
+        c = got.view(np.float16)[rows].astype(np.float64)
+        err = np.max(np.abs(c - ref)) / np.max(np.abs(ref))
+        assert err <= 1e-3, err
+
+
+def test_noalloc_rejects_bad_arguments(q):
+    L = _lib.lib()
+    rc = L.madi_q8_gemm_noalloc(0x100000, 0x100000, 0x100000, 0x100000, None, 16, 100, 1280, 0)
+    assert rc == -5  # n % 32
+    rc = L.madi_q8_gemm_noalloc(None, 0x100000, 0x100000, 0x100000, None, 16, 256, 1280, 0)
+    assert rc == -6
+
+
+def test_noalloc_under_graph_capture(q):
+    """A fresh library (its growable workspace back at the 4 MiB of madi_init)
+    captures the fc2 + bias GEMM at M = 1500, whose 15 MiB of split-K partials
+    madi_q8_gemm could only get by growing the workspace, which capture
+    forbids; the allocation-free entry point needs no buffer.  Every replay,
+    with eager work between them, equals the eager result."""
+    m, n, k = 1500, 1280, 5120
+    say(f"noalloc graph capture m={m} n={n} k={k}")
+    _lib.lib().madi_cleanup()
+    q.init()
+    a, qs, sc = synth.gemm_case(55, m, n, k)
+    bias = np.random.default_rng(56).standard_normal(n).astype(np.float32)
+    w = q.upload_q8(qs, sc)
+    a_d, b_d = dev_f16(a), torch.from_numpy(bias).cuda()
+    c = torch.empty((m, n), dtype=torch.int16, device="cuda")
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            q.init(side)
+            _lib.call("madi_q8_gemm_noalloc", a_d.data_ptr(), w.qs, w.scales, c.data_ptr(),
+                      b_d.data_ptr(), m, n, k, _lib.EPI_BIAS)
+    q.init()
+    want = run(q, "madi_q8_gemm", a_d, w, b_d, m, n, k, _lib.EPI_BIAS)
+    for rep in range(3):
+        c.fill_(-1)
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(c.cpu().numpy(), want), rep
+        # eager work between replays: a smaller split shape on the same scratch
+        a2, qs2, sc2 = synth.gemm_case(57 + rep, 257, 1280, 5120)
+        w2 = q.upload_q8(qs2, sc2)
+        a2_d = dev_f16(a2)
+        assert np.array_equal(run(q, "madi_q8_gemm_noalloc", a2_d, w2, None, 257, 1280, 5120, 0),
+                              run(q, "madi_q8_gemm", a2_d, w2, None, 257, 1280, 5120, 0))
