@@ -276,6 +276,9 @@ def config_decode_token(torch, stream, q8, reps=20):
     step_bytes = (DEC_LAYERS * sum(n * k + n * (k // 32) * 2 for n, k in shapes)
                   + VOCAB * DIM + VOCAB * (DIM // 32) * 2)
 
+    f_gelu = q8.getFunction("gemv_q8_bias_gelu")  # the handles decoder.zig resolves once
+    f_res = q8.getFunction("gemv_q8_bias_res")
+
     def token(i):
         layers, vocab = sets[i % 2]
         for w in layers:
@@ -283,8 +286,8 @@ def config_decode_token(torch, stream, q8, reps=20):
             q8.kGemvQ8(mo, ao, w[1], d, d)
             q8.kGemvQ8Bias(q, xb, w[2], bd, d, d)
             q8.kGemvQ8(mo, ao, w[3], d, d)
-            q8.kGemvQ8BiasEpi("gemv_q8_bias_gelu", mh, xb, w[4], bm, mlp, d)
-            q8.kGemvQ8BiasEpi("gemv_q8_bias_res", x, mh, w[5], bd, d, mlp)
+            q8.kGemvQ8BiasEpi(f_gelu, mh, xb, w[4], bm, mlp, d)
+            q8.kGemvQ8BiasEpi(f_res, x, mh, w[5], bd, d, mlp)
         q8.kLogitGemv(logits, vocab.qs, vocab.scales, xb, VOCAB, DIM)
 
     token(0)

@@ -127,7 +127,8 @@ uint64_t madi_q8_fnv(uint64_t seed, const void *qs, size_t nq, const void *scale
 /* ---- ops (device pointers, panel-layout weights) ---------------------------- */
 /* Q8 -> F16 [K][N] transposed dequant, bit-exact fp16_rne(q * s).  Replaces
  * kDeq (engine/metal/encoder.zig:154-159) and deqW16 (transcribe.zig:4387-4393),
- * kernel dequant_q8_f16 (engine/metal/kernels/q8_gemm.metal:12-27). */
+ * kernel dequant_q8_f16 (engine/metal/kernels/q8_gemm.metal:12-27).  Deferred
+ * by default: see "Deferred dequantisation" below. */
 int madi_q8_dequant_f16(void *wdq, const void *qs, const void *scales, uint32_t n,
                         uint32_t k);
 
@@ -198,6 +199,48 @@ int madi_q8_gemv_f16x(float *out, const void *x_f16, const void *qs, const void 
 int madi_q8_pproj(float *out, const float *in, const void *qs, const void *scales,
                   uint32_t m, uint32_t n, uint32_t k);
 
+/* ---- kernel handles and the engine's handle-taking wrappers ---------------- */
+/* Handle for one of this path's kernel names (replaces mtl_get_function,
+ * metal_backend.h:46, behind mtl.getFunction, metal_backend.zig:61-65):
+ * "dequant_q8_f16", "m4_gemm_nn", "m4_gemm_bias", "m4_gemm_bias_gelu",
+ * "gemv_q8", "gemv_q8_bias", "gemv_q8_bias_gelu", "gemv_q8_bias_res",
+ * "gemv_q8_qkv", "logit_gemv_q8", "gpu_emb_lookup_q8",
+ * "emb_lookup_indirect_q8", "emb_pe_rows_q8", "mul_mm_q8".  Another name
+ * fails with MADI_ERR_ARG (FunctionNotFound).  Needs no device. */
+int madi_get_function(const char *name, int *out_id);
+/* kM4 / kM4Bias (engine/metal/encoder.zig:125-136) with the handle the engine
+ * resolved: m4_gemm_nn (bias ignored), m4_gemm_bias or m4_gemm_bias_gelu, on
+ * an F16 weight b [K][N]; same as madi_f16_gemm with that epilogue. */
+int madi_m4_gemm(int func, const void *a, const void *b, void *c, const float *bias, uint32_t m,
+                 uint32_t n, uint32_t k);
+/* kGemvQ8BiasEpi (engine/metal/decoder.zig:176-181) with its handle:
+ * gemv_q8_bias_gelu or gemv_q8_bias_res (or gemv_q8_bias). */
+int madi_q8_gemv_epi(int func, float *out, const float *x, const void *qs, const void *scales,
+                     const float *bias, uint32_t n, uint32_t k);
+/* proj (engine/metal/decoder.zig:337-341): out[B][N] (f32) = in[B][K] (f32)
+ * . w16, w16 the F16 [K][N] copy deqW16 made of a Q8 weight.  A recorded
+ * copy (below) runs madi_q8_pproj on the Q8 weight; a true F16 weight is
+ * staged to f16 in stage16 ([B][K] f16, the BScratch in16 buffer) and
+ * multiplied by a library GEMM with an f32 result. */
+int madi_proj_f16w(float *out, const float *in, const void *w16, void *stage16, uint32_t m,
+                   uint32_t n, uint32_t k);
+
+/* Deferred dequantisation.  madi_q8_dequant_f16 (kDeq, deqW16) records
+ * (wdq -> Q8 weight) instead of writing wdq.  madi_f16_gemm, madi_m4_gemm,
+ * madi_matmul_f16 (alpha 1, beta 0) and madi_proj_f16w whose F16 weight is
+ * exactly a recorded wdq of the recorded shape run the fused Q8 kernels on
+ * the Q8 weight, so the encoder's kDeq + kM4 / kM4Bias pairs
+ * (encoder.zig:262-301) and the batched decoder's deqW16 + proj need no
+ * change to run them.  wdq is written ("materialised") before anything in
+ * this library could observe it: another op reading it, madi_download of it,
+ * a write into or madi_free of the Q8 source, a partial overwrite of wdq; a
+ * full overwrite or madi_free of wdq drops the record.  Kernels outside this
+ * library that read wdq need madi_q8_materialize(wdq) first (NULL: every
+ * record).  madi_set_deferred_dequant(0) materialises every record and makes
+ * madi_q8_dequant_f16 write wdq at once (the default is 1). */
+int madi_q8_materialize(void *wdq);
+int madi_set_deferred_dequant(int on);
+
 /* ---- plain fp16 GEMMs (pre-dequantised F16 weights) ------------------------ */
 /* C[M][N] (f16) = epi(A[M][K] (f16) . B[K][N] (f16)), all row-major, fp32
  * accumulation.  Replaces kM4 / kM4Bias (engine/metal/encoder.zig:125-136) ->
@@ -224,6 +267,15 @@ int madi_q8_emb_lookup(float *out, const void *qs, const void *scales,
 int madi_q8_emb_lookup_indirect(float *out, const void *qs, const void *scales,
                                 const uint32_t *tokens, const uint32_t *pos_ptr,
                                 uint32_t vocab, uint32_t dim);
+/* Sequence prefill's embedding rows from the panel layout: out[m][d] =
+ * f32(q) * f32(s) of row tokens[m] + pe[(pos0 + m) * dim + d] for m < M
+ * (f32 out [M][dim], one rounding: the add).  Replaces emb_pe_rows_q8
+ * (engine/metal/kernels/decoder_ops.metal:614-633) behind prefillEmbed
+ * (engine/metal/decoder.zig:460-467), which reads the tied tok_emb.  pe must
+ * hold rows up to pos0 + M - 1 (the caller's bound, as in the reference); a
+ * token >= vocab leaves its row untouched.  out and pe 16-byte aligned. */
+int madi_q8_emb_pe_rows(float *out, const void *qs, const void *scales, const uint32_t *tokens,
+                        const float *pe, uint32_t dim, uint32_t pos0, uint32_t m, uint32_t vocab);
 
 #ifdef __cplusplus
 }

@@ -55,10 +55,17 @@ SIGNATURES = {
     "madi_q8_logit_gemv": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_gemv_f16x": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _I]),
     "madi_q8_pproj": (_I, [_P, _P, _P, _P, _U32, _U32, _U32]),
+    "madi_get_function": (_I, [ctypes.c_char_p, ctypes.POINTER(_I)]),
+    "madi_m4_gemm": (_I, [_I, _P, _P, _P, _P, _U32, _U32, _U32]),
+    "madi_q8_gemv_epi": (_I, [_I, _P, _P, _P, _P, _P, _U32, _U32]),
+    "madi_proj_f16w": (_I, [_P, _P, _P, _P, _U32, _U32, _U32]),
+    "madi_q8_materialize": (_I, [_P]),
+    "madi_set_deferred_dequant": (_I, [_I]),
     "madi_f16_gemm": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _I]),
     "madi_matmul_f16": (_I, [_P, _P, _P, _I, _I, _I, ctypes.c_float, ctypes.c_float]),
     "madi_q8_emb_lookup": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_emb_lookup_indirect": (_I, [_P, _P, _P, _P, _P, _U32, _U32]),
+    "madi_q8_emb_pe_rows": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32]),
 }
 
 

@@ -29,6 +29,31 @@ void f16gemm_cleanup();
 // scratch array and clears its counters (madi_init).
 int gemm_scratch_init();
 
+// Deferred dequantisation (boundary.hip).  madi_q8_dequant_f16 records
+// (wdq -> Q8 weight) instead of writing wdq; an F16 GEMM whose weight is
+// exactly a recorded wdq runs the fused Q8 kernel.  Every entry point calls
+// deferred_before_write on the device memory it writes (records whose wdq it
+// overwrites are retired; records whose Q8 source it overwrites are
+// materialised first) and deferred_before_read on F16 memory it reads other
+// than through that lookup (a recorded wdq is materialised first).
+// deferred_record returns 1 when it recorded, 0 when deferral is off (the
+// caller dequantises now), or an error code.
+int deferred_record(void *wdq, const void *qs, const void *sc, uint32_t n, uint32_t k);
+bool deferred_lookup(const void *wdq, uint32_t n, uint32_t k, const void **qs, const void **sc);
+int deferred_before_write(const void *ptr, size_t bytes);
+int deferred_before_read(const void *ptr, size_t bytes);
+// madi_free: records whose Q8 source lies in the freed memory are materialised,
+// records whose wdq lies in it are dropped.  Returns 1 when it launched a
+// dequantisation that reads the memory about to be freed.
+int deferred_before_free(const void *ptr, size_t bytes);
+// Materialises every record and forgets them (madi_cleanup).
+int deferred_flush_all();
+// Launches the transposed dequantisation Q8 -> F16 [K][N] (layout.hip).
+int dequant_launch(void *wdq, const void *qs, const void *sc, uint32_t n, uint32_t k);
+// Bytes from p to the end of the live madi_alloc allocation that contains p,
+// 0 if no such allocation contains it.
+size_t alloc_extent(const void *p);
+
 inline bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
 // ---------------------------------------------------------------- device side

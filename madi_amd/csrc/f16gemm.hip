@@ -45,6 +45,37 @@ int gemm_f16(const char *what, const void *a, const void *b, void *c, uint32_t m
   return MADI_OK;
 }
 
+// C[M][N] (f32) = A[M][K] (f16) . B[K][N] (f16), row-major, fp32 accumulation
+// (rocBLAS with f16 inputs and an f32 result).
+int gemm_f16_f32out(const char *what, const void *a, const void *b, float *c, uint32_t m,
+                    uint32_t n, uint32_t k) {
+  rocblas_handle h;
+  if (int rc = blas(&h, what)) return rc;
+  const float alpha = 1.0f, beta = 0.0f;
+  const rocblas_status st = rocblas_gemm_ex(
+      h, rocblas_operation_none, rocblas_operation_none, (rocblas_int)n, (rocblas_int)m,
+      (rocblas_int)k, &alpha, b, rocblas_datatype_f16_r, (rocblas_int)n, a, rocblas_datatype_f16_r,
+      (rocblas_int)k, &beta, c, rocblas_datatype_f32_r, (rocblas_int)n, c, rocblas_datatype_f32_r,
+      (rocblas_int)n, rocblas_datatype_f32_r, rocblas_gemm_algo_standard, 0, 0);
+  if (st != rocblas_status_success)
+    return fail(MADI_ERR_DISPATCH, "%s: rocblas_gemm_ex failed (%s)", what, rocblas_status_to_string(st));
+  return MADI_OK;
+}
+
+// The operands the fused Q8 GEMM needs (16-byte aligned A, C and bias, whole
+// 32-row panels); otherwise a recorded weight is materialised and the library
+// GEMM runs.
+inline bool fusable(const void *a, const void *c, const float *bias, uint32_t n) {
+  return aligned(a, 16) && aligned(c, 16) && (!bias || aligned(bias, 16)) && n % kPanelRows == 0;
+}
+
+// dst[i] = f16(src[i]) (round to nearest even), the engine's f32 -> f16 staging
+__global__ __launch_bounds__(256) void to_f16_kernel(f16 *__restrict__ dst,
+                                                     const float *__restrict__ src, size_t count) {
+  const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < count) dst[i] = (f16)src[i];
+}
+
 // c[r][col] = f16(epi(float(c[r][col]) + bias[col])), m4_gemm.metal:79-85 / 108-114
 template <bool GELU>
 __global__ __launch_bounds__(256) void bias_epilogue_kernel(f16 *__restrict__ c,
@@ -78,6 +109,15 @@ extern "C" int madi_f16_gemm(const void *a, const void *b, void *c, const float 
   if (!aligned(a, 2) || !aligned(b, 2) || !aligned(c, 2) || (bias && !aligned(bias, 4)))
     return fail(MADI_ERR_ALIGN, "madi_f16_gemm: misaligned operand");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_f16_gemm: madi_init has not succeeded");
+  // b is the F16 [K][N] that kDeq recorded for a Q8 weight [N][K]: the fused Q8
+  // GEMM runs on that weight (one rounding of acc + bias, the Q8-direct
+  // kernel's epilogue, m4_gemm.metal:180-186) and b is never written
+  const void *qs, *sc;
+  if (fusable(a, c, bias, n) && deferred_lookup(b, n, k, &qs, &sc))
+    return madi_q8_gemm(a, qs, sc, c, bias, m, n, k, epilogue);
+  if (int rc = deferred_before_read(a, (size_t)m * k * 2)) return rc;
+  if (int rc = deferred_before_read(b, (size_t)k * n * 2)) return rc;
+  if (int rc = deferred_before_write(c, (size_t)m * n * 2)) return rc;
   if (int rc = gemm_f16("madi_f16_gemm", a, b, c, m, n, k, 1.0f, 0.0f)) return rc;
   if (epilogue == MADI_EPI_NONE) return MADI_OK;
   const size_t count = (size_t)m * n;
@@ -99,5 +139,42 @@ extern "C" int madi_matmul_f16(const void *a, const void *b, void *c, int m, int
   if (!aligned(a, 2) || !aligned(b, 2) || !aligned(c, 2))
     return fail(MADI_ERR_ALIGN, "madi_matmul_f16: misaligned operand");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_matmul_f16: madi_init has not succeeded");
+  const void *qs, *sc;
+  if (alpha == 1.0f && beta == 0.0f && fusable(a, c, nullptr, (uint32_t)n) &&
+      deferred_lookup(b, (uint32_t)n, (uint32_t)k, &qs, &sc))
+    return madi_q8_gemm(a, qs, sc, c, nullptr, (uint32_t)m, (uint32_t)n, (uint32_t)k, MADI_EPI_NONE);
+  const size_t mn = (size_t)m * n * 2;
+  if (int rc = deferred_before_read(a, (size_t)m * k * 2)) return rc;
+  if (int rc = deferred_before_read(b, (size_t)k * n * 2)) return rc;
+  if (beta != 0.0f)
+    if (int rc = deferred_before_read(c, mn)) return rc;
+  if (int rc = deferred_before_write(c, mn)) return rc;
   return gemm_f16("madi_matmul_f16", a, b, c, (uint32_t)m, (uint32_t)n, (uint32_t)k, alpha, beta);
+}
+
+extern "C" int madi_proj_f16w(float *out, const float *in, const void *w16, void *stage16,
+                              uint32_t m, uint32_t n, uint32_t k) {
+  if (!out || !in || !w16) return fail(MADI_ERR_NULL, "madi_proj_f16w: null pointer");
+  if (m == 0 || n == 0 || k == 0 || m > 0x7fffffffu || n > 0x7fffffffu || k > 0x7fffffffu)
+    return fail(MADI_ERR_SHAPE, "madi_proj_f16w: m=%u n=%u k=%u", m, n, k);
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_proj_f16w: madi_init has not succeeded");
+  // w16 is a recorded F16 copy of a Q8 weight (deqW16 at decode start): the
+  // batched projection runs from the Q8 weight, one kernel
+  const void *qs, *sc;
+  if (aligned(in, 16) && aligned(out, 4) && deferred_lookup(w16, n, k, &qs, &sc))
+    return madi_q8_pproj(out, in, qs, sc, m, n, k);
+  // a true F16 weight: the reference's f32 -> f16 staging, then an f16 GEMM
+  // with an f32 result
+  if (!stage16) return fail(MADI_ERR_NULL, "madi_proj_f16w: null staging buffer for an F16 weight");
+  if (!aligned(w16, 2) || !aligned(stage16, 2) || !aligned(in, 4) || !aligned(out, 4))
+    return fail(MADI_ERR_ALIGN, "madi_proj_f16w: misaligned operand");
+  const size_t count = (size_t)m * k;
+  if (int rc = deferred_before_read(in, count * 4)) return rc;
+  if (int rc = deferred_before_read(w16, (size_t)k * n * 2)) return rc;
+  if (int rc = deferred_before_write(stage16, count * 2)) return rc;
+  if (int rc = deferred_before_write(out, (size_t)m * n * 4)) return rc;
+  hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream(),
+                     static_cast<f16 *>(stage16), in, count);
+  if (int rc = check_launch("madi_proj_f16w(stage)")) return rc;
+  return gemm_f16_f32out("madi_proj_f16w", stage16, w16, out, m, n, k);
 }

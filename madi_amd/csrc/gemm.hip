@@ -832,6 +832,8 @@ int q8_gemm(const char *what, const void *a, const void *qs, const void *scales,
       (bias && !aligned(bias, 16)))
     return fail(MADI_ERR_ALIGN, "%s: a/qs/scales/c/bias need 16-byte alignment", what);
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);
+  if (int rc = deferred_before_read(a, (size_t)m * k * 2)) return rc;
+  if (int rc = deferred_before_write(c, (size_t)m * n * 2)) return rc;
   const f16 *A = static_cast<const f16 *>(a);
   const uint8_t *Q = static_cast<const uint8_t *>(qs);
   const f16 *S = static_cast<const f16 *>(scales);

@@ -306,6 +306,19 @@ int launch(const char *what, const GemvArgs &a) {
   if (!aligned(a.qs, 16) || !aligned(a.sc, 2) || !aligned(a.x, 16))
     return fail(MADI_ERR_ALIGN, "%s: qs and x need 16-byte alignment", what);
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);
+  if (int rc = deferred_before_read(a.x, (size_t)a.k * sizeof(XT))) return rc;
+  if (MODE == kQkv) {
+    // q_out [D], and one row of each cache at a position only the device
+    // knows: somewhere in the allocation from kc (vc) on, if the library
+    // allocated it, else at least the first row
+    const size_t row = (size_t)(a.n / 3) * 4;
+    const size_t kext = alloc_extent(a.kc), vext = alloc_extent(a.vc);
+    if (int rc = deferred_before_write(a.out, row)) return rc;
+    if (int rc = deferred_before_write(a.kc, kext > row ? kext : row)) return rc;
+    if (int rc = deferred_before_write(a.vc, vext > row ? vext : row)) return rc;
+  } else if (int rc = deferred_before_write(a.out, (size_t)a.n * 4)) {
+    return rc;
+  }
   const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows, C = a.k / kChunkK;
   // Few panels and a long K (the 5120-wide FFN down projection: 40 panels)
   // leave most CUs idle and each wave with a long chain of loads: split K

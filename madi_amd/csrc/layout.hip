@@ -129,6 +129,8 @@ extern "C" int madi_q8_repack(void *dst_qs, void *dst_scales, const void *qs, co
   if (overlaps(dst_qs, nq, qs, nq) || overlaps(dst_scales, ns * 2, scales, ns * 2))
     return fail(MADI_ERR_ARG, "madi_q8_repack: source and destination overlap");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_repack: madi_init has not succeeded");
+  if (int rc = deferred_before_write(dst_qs, nq)) return rc;
+  if (int rc = deferred_before_write(dst_scales, ns * 2)) return rc;
   const size_t units = nq / 16;
   hipLaunchKernelGGL(q8_repack_qs_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0,
                      stream(), static_cast<uint8_t *>(dst_qs), static_cast<const int8_t *>(qs), n,
@@ -198,6 +200,8 @@ extern "C" int madi_q8_quantize(void *dst_qs, void *dst_scales, const void *w_f1
     return fail(MADI_ERR_ALIGN, "madi_q8_quantize: qs and w need 16-byte alignment");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_quantize: madi_init has not succeeded");
   const size_t blocks = (size_t)n * (k / 32);
+  if (int rc = deferred_before_write(dst_qs, (size_t)n * k)) return rc;
+  if (int rc = deferred_before_write(dst_scales, blocks * 2)) return rc;
   hipLaunchKernelGGL(q8_quantize_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
                      stream(), static_cast<uint8_t *>(dst_qs), static_cast<uint16_t *>(dst_scales),
                      static_cast<const uint16_t *>(w_f16), n, k, blocks);
@@ -244,6 +248,20 @@ __global__ __launch_bounds__(256) void q8_dequant_f16_kernel(f16 *__restrict__ o
   }
 }
 
+namespace madi {
+int dequant_launch(void *wdq, const void *qs, const void *scales, uint32_t n, uint32_t k) {
+  const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
+  const uint32_t units = kPanelRows * (k / 16);
+  hipLaunchKernelGGL(q8_dequant_f16_kernel, dim3((units + 255) / 256, np), dim3(256), 0,
+                     stream(), static_cast<f16 *>(wdq), static_cast<const uint8_t *>(qs),
+                     static_cast<const f16 *>(scales), n, k);
+  return check_launch("madi_q8_dequant_f16");
+}
+}  // namespace madi
+
+// kDeq / deqW16.  With deferral on (the default) this records the pair and
+// returns: the F16 GEMM that consumes wdq runs the fused Q8 kernel instead,
+// and wdq is written only if something else reads it (boundary.hip).
 extern "C" int madi_q8_dequant_f16(void *wdq, const void *qs, const void *scales, uint32_t n,
                                    uint32_t k) {
   if (!wdq || !qs || !scales) return fail(MADI_ERR_NULL, "madi_q8_dequant_f16: null pointer");
@@ -251,12 +269,9 @@ extern "C" int madi_q8_dequant_f16(void *wdq, const void *qs, const void *scales
   if (!aligned(qs, 16) || !aligned(scales, 2) || !aligned(wdq, 2))
     return fail(MADI_ERR_ALIGN, "madi_q8_dequant_f16: qs needs 16-byte alignment");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_dequant_f16: madi_init has not succeeded");
-  const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
-  const uint32_t units = kPanelRows * (k / 16);
-  hipLaunchKernelGGL(q8_dequant_f16_kernel, dim3((units + 255) / 256, np), dim3(256), 0,
-                     stream(), static_cast<f16 *>(wdq), static_cast<const uint8_t *>(qs),
-                     static_cast<const f16 *>(scales), n, k);
-  return check_launch("madi_q8_dequant_f16");
+  const int rec = deferred_record(wdq, qs, scales, n, k);
+  if (rec != 0) return rec < 0 ? rec : MADI_OK;
+  return dequant_launch(wdq, qs, scales, n, k);
 }
 
 // ------------------------------------------------------------------ embedding rows
@@ -293,9 +308,69 @@ static int emb_common(const char *what, float *out, const void *qs, const void *
   if (!aligned(qs, 16) || !aligned(scales, 2) || !aligned(out, 4))
     return fail(MADI_ERR_ALIGN, "%s: misaligned pointer", what);
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);
+  if (int rc = deferred_before_write(out, (size_t)dim * 4)) return rc;
   hipLaunchKernelGGL(q8_emb_row_kernel, dim3(1), dim3(256), 0, stream(), out,
                      static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), tok_ptr,
                      tokens, pos_ptr, n_rows, dim);
+  return check_launch(what);
+}
+
+// emb_pe_rows_q8 semantics (engine/metal/kernels/decoder_ops.metal:614-633), the
+// sequence prefill's embedding (decoder.zig:460-467): out[m][d] =
+// f32(q) * f32(s) of row tokens[m] + pe[(pos0 + m) * dim + d].  One workgroup
+// per row; a thread takes one 16-byte unit of the panel layout (16
+// consecutive d of one quantisation block), so each row is read as whole
+// units and written as 64-byte runs.  The product is exact in f32 (8 x 11
+// significant bits), so the one rounding is the add, as in the reference.  A
+// token >= n_rows leaves its row untouched.
+__global__ __launch_bounds__(256) void q8_emb_pe_rows_kernel(
+    float *__restrict__ out, const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
+    const uint32_t *__restrict__ tokens, const float *__restrict__ pe, uint32_t n_rows,
+    uint32_t dim, uint32_t pos0) {
+  const uint32_t m = blockIdx.x;
+  const uint32_t tok = tokens[m];
+  if (tok >= n_rows) return;
+  const uint32_t p = tok / kPanelRows, r = tok % kPanelRows, R = panel_rows(n_rows, p);
+  const float *per = pe + (size_t)(pos0 + m) * dim;
+  float *o = out + (size_t)m * dim;
+  for (uint32_t u = threadIdx.x; u < dim / 16; u += blockDim.x) {
+    const uint32_t d0 = u * 16, c = d0 / kChunkK, h = (d0 % kChunkK) / 32, j = (d0 % 32) / 16;
+    const u32x4 w = *reinterpret_cast<const u32x4 *>(qs + panel_chunk_qs(dim, p, R, c) +
+                                                     ((2 * j + h) * R + r) * 16);
+    const float s = (float)sc[panel_chunk_sc(dim, p, R, c) + h * R + r];
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const f32x4 e = *reinterpret_cast<const f32x4 *>(per + d0 + 4 * v);
+      f32x4 res;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const int q = (int)((words[v] >> (8 * b)) & 0xffu) - 128;
+        res[b] = (float)q * s + e[b];
+      }
+      *reinterpret_cast<f32x4 *>(o + d0 + 4 * v) = res;
+    }
+  }
+}
+
+extern "C" int madi_q8_emb_pe_rows(float *out, const void *qs, const void *scales,
+                                   const uint32_t *tokens, const float *pe, uint32_t dim,
+                                   uint32_t pos0, uint32_t m, uint32_t vocab) {
+  const char *what = "madi_q8_emb_pe_rows";
+  if (!out || !qs || !scales || !tokens || !pe) return fail(MADI_ERR_NULL, "%s: null pointer", what);
+  if (dim == 0 || dim % kChunkK) return fail(MADI_ERR_SHAPE, "%s: dim=%u must be a positive multiple of 64", what, dim);
+  if (vocab == 0) return fail(MADI_ERR_SHAPE, "%s: empty table", what);
+  if (m == 0) return MADI_OK;
+  if (m > 65535u) return fail(MADI_ERR_SHAPE, "%s: m=%u exceeds 65535 rows", what, m);
+  if ((uint64_t)vocab * dim >= (1ull << 32))
+    return fail(MADI_ERR_SHAPE, "%s: vocab=%u dim=%u exceeds the 4 GiB table limit", what, vocab, dim);
+  if (!aligned(qs, 16) || !aligned(scales, 2) || !aligned(out, 16) || !aligned(pe, 16))
+    return fail(MADI_ERR_ALIGN, "%s: qs, out and pe need 16-byte alignment", what);
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);
+  if (int rc = deferred_before_write(out, (size_t)m * dim * 4)) return rc;
+  hipLaunchKernelGGL(q8_emb_pe_rows_kernel, dim3(m), dim3(dim / 16 < 256 ? 64 * ((dim / 16 + 63) / 64) : 256),
+                     0, stream(), out, static_cast<const uint8_t *>(qs),
+                     static_cast<const f16 *>(scales), tokens, pe, vocab, dim, pos0);
   return check_launch(what);
 }
 

@@ -7,6 +7,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <map>
+
 #include "common.h"
 
 namespace madi {
@@ -28,6 +30,9 @@ size_t g_ws_bytes = 0;
 constexpr int kMaxRetired = 32;
 void *g_retired[kMaxRetired];
 int g_nretired = 0;
+// Live madi_alloc allocations (base -> bytes), for the deferred
+// dequantisation's free and write extents.
+std::map<uintptr_t, size_t> g_allocs;
 
 void free_workspace() {
   if (g_ws || g_nretired) (void)hipDeviceSynchronize();
@@ -91,6 +96,15 @@ int check_launch(const char *what) {
   return MADI_OK;
 }
 
+size_t alloc_extent(const void *ptr) {
+  const uintptr_t p = reinterpret_cast<uintptr_t>(ptr);
+  auto it = g_allocs.upper_bound(p);
+  if (it == g_allocs.begin()) return 0;
+  --it;
+  const uintptr_t end = it->first + it->second;
+  return p < end ? end - p : 0;
+}
+
 bool initialized() { return g_init; }
 int cu_count() { return g_cu_count; }
 hipStream_t stream() { return g_stream; }
@@ -136,6 +150,7 @@ extern "C" int madi_init(void) {
 
 extern "C" void madi_cleanup(void) {
   if (!g_init) return;
+  (void)deferred_flush_all();
   (void)hipStreamSynchronize(g_stream);
   free_workspace();
   f16gemm_cleanup();
@@ -155,11 +170,16 @@ extern "C" void *madi_alloc(size_t size) {
     fail(MADI_ERR_ALLOC, "madi_alloc(%zu): %s", size, hipGetErrorString(e));
     return nullptr;
   }
+  g_allocs[reinterpret_cast<uintptr_t>(p)] = size;
   return p;
 }
 
 extern "C" void madi_free(void *ptr) {
   if (!ptr || !g_init) return;
+  const size_t ext = alloc_extent(ptr);
+  // a dequantisation launched from the memory being freed finishes first
+  if (deferred_before_free(ptr, ext ? ext : 1) > 0) (void)hipStreamSynchronize(g_stream);
+  g_allocs.erase(reinterpret_cast<uintptr_t>(ptr));
   (void)hipFree(ptr);
 }
 
@@ -167,6 +187,7 @@ extern "C" int madi_upload(void *dst, const void *src, size_t size) {
   if (!g_init) return fail(MADI_ERR_NOT_INIT, "madi_upload: madi_init has not succeeded");
   if (size == 0) return MADI_OK;
   if (!dst || !src) return fail(MADI_ERR_NULL, "madi_upload: null pointer");
+  if (int rc = deferred_before_write(dst, size)) return rc;
   hipError_t e = hipMemcpyAsync(dst, src, size, hipMemcpyHostToDevice, g_stream);
   if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
   if (e != hipSuccess) return fail(MADI_ERR_SYNC, "madi_upload: %s", hipGetErrorString(e));
@@ -177,6 +198,7 @@ extern "C" int madi_download(void *dst, const void *src, size_t size) {
   if (!g_init) return fail(MADI_ERR_NOT_INIT, "madi_download: madi_init has not succeeded");
   if (size == 0) return MADI_OK;
   if (!dst || !src) return fail(MADI_ERR_NULL, "madi_download: null pointer");
+  if (int rc = deferred_before_read(src, size)) return rc;
   hipError_t e = hipMemcpyAsync(dst, src, size, hipMemcpyDeviceToHost, g_stream);
   if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
   if (e != hipSuccess) return fail(MADI_ERR_SYNC, "madi_download: %s", hipGetErrorString(e));

@@ -345,6 +345,8 @@ extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const 
   if (!aligned(qs, 16) || !aligned(scales, 2) || !aligned(in, 16) || !aligned(out, 4))
     return fail(MADI_ERR_ALIGN, "madi_q8_pproj: qs and in need 16-byte alignment");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_pproj: madi_init has not succeeded");
+  if (int rc = deferred_before_read(in, (size_t)m * k * 4)) return rc;
+  if (int rc = deferred_before_write(out, (size_t)m * n * 4)) return rc;
   const Proj a{out, in, static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), m, n, k};
   // a batch of up to 8 or 16 rows loads only those activation rows
   if (m <= 8) return launch_rows<8>(a);

@@ -46,6 +46,29 @@ def sync() -> None:
     call("madi_sync")
 
 
+def getFunction(name: str) -> int:
+    """mtl.getFunction (metal_backend.zig:61-65) for this path's kernel names:
+    the handle the handle-taking wrappers below expect."""
+    import ctypes
+    out = ctypes.c_int(-1)
+    check(lib().madi_get_function(name.encode(), ctypes.byref(out)), f"madi_get_function({name})")
+    return out.value
+
+
+def _fn(f) -> int:
+    return getFunction(f) if isinstance(f, str) else int(f)
+
+
+def materialize(wdq=None) -> None:
+    """Write a deferred kDeq / deqW16 result into wdq now (None: every one), for
+    a reader outside the library (e.g. a torch copy of wdq)."""
+    call("madi_q8_materialize", ptr(wdq))
+
+
+def set_deferred_dequant(on: bool) -> None:
+    call("madi_set_deferred_dequant", 1 if on else 0)
+
+
 @dataclass
 class Q8:
     """A panel-layout Q8 weight on the device: {qs, scales} as in
@@ -128,7 +151,9 @@ def fnv(seed: int, qs: np.ndarray, scales: np.ndarray) -> int:
 
 # ---- encoder.zig -----------------------------------------------------------
 def kDeq(wdq, w: Q8, n: int, k: int) -> None:
-    """encoder.zig:154-159: Q8 [N][K] -> F16 [K][N] (dequant_q8_f16)."""
+    """encoder.zig:154-159: Q8 [N][K] -> F16 [K][N] (dequant_q8_f16).  Deferred:
+    an F16 GEMM on wdq runs the fused Q8 kernel; materialize(wdq) before reading
+    wdq outside the library."""
     call("madi_q8_dequant_f16", ptr(wdq), w.qs, w.scales, n, k)
 
 
@@ -149,16 +174,16 @@ def kGemmQ8Bias(a, w: Q8, c, bias, m: int, n: int, k: int, gelu: bool = False) -
          EPI_BIAS_GELU if gelu else EPI_BIAS)
 
 
-def kM4(a, b, c, m: int, n: int, k: int) -> None:
-    """encoder.zig:125-130 (m4_gemm_nn): C = A . B, f16 [M][K] . [K][N] (an F16
-    weight, e.g. the output of kDeq)."""
-    call("madi_f16_gemm", ptr(a), ptr(b), ptr(c), None, m, n, k, EPI_NONE)
+def kM4(f, a, b, c, m: int, n: int, k: int) -> None:
+    """encoder.zig:125-130: C = A . B, f16 [M][K] . [K][N], f = the m4_gemm_nn
+    handle (or its name).  b is an F16 weight or the wdq a kDeq just recorded
+    (then the fused Q8 GEMM runs)."""
+    call("madi_m4_gemm", _fn(f), ptr(a), ptr(b), ptr(c), None, m, n, k)
 
 
-def kM4Bias(a, b, c, bias, m: int, n: int, k: int, gelu: bool = False) -> None:
-    """encoder.zig:131-136 (m4_gemm_bias / m4_gemm_bias_gelu)."""
-    call("madi_f16_gemm", ptr(a), ptr(b), ptr(c), ptr(bias), m, n, k,
-         EPI_BIAS_GELU if gelu else EPI_BIAS)
+def kM4Bias(f, a, b, c, bias, m: int, n: int, k: int) -> None:
+    """encoder.zig:131-136, f = the m4_gemm_bias or m4_gemm_bias_gelu handle."""
+    call("madi_m4_gemm", _fn(f), ptr(a), ptr(b), ptr(c), ptr(bias), m, n, k)
 
 
 def matmulF16Batched(a, b, c, m: int, n: int, k: int, alpha: float = 1.0,
@@ -178,18 +203,23 @@ def kGemvQ8Bias(out, x, w: Q8, bias, n: int, k: int) -> None:
     call("madi_q8_gemv_bias", ptr(out), ptr(x), w.qs, w.scales, ptr(bias), n, k)
 
 
-def kGemvQ8BiasEpi(f: str, out, x, w: Q8, bias, n: int, k: int) -> None:
-    """decoder.zig:176-181; f = "gemv_q8_bias_gelu" or "gemv_q8_bias_res"."""
-    name = {"gemv_q8_bias_gelu": "madi_q8_gemv_bias_gelu",
-            "gemv_q8_bias_res": "madi_q8_gemv_bias_res"}[f]
-    call(name, ptr(out), ptr(x), w.qs, w.scales, ptr(bias), n, k)
+def kGemvQ8BiasEpi(f, out, x, w: Q8, bias, n: int, k: int) -> None:
+    """decoder.zig:176-181; f = the gemv_q8_bias_gelu or gemv_q8_bias_res handle
+    (or its name)."""
+    call("madi_q8_gemv_epi", _fn(f), ptr(out), ptr(x), w.qs, w.scales, ptr(bias), n, k)
 
 
 def pproj(in_f32, w: Q8, out_f32, M: int, N: int, Kk: int) -> None:
     """decoder.zig:427-432 (pproj: kDeq + kCvt32 + matmulF16Batched + kCvt16)
-    as one fused kernel; also serves proj (decoder.zig:337-341) straight from
-    the Q8 weights.  in_f32 [M][Kk] -> out_f32 [M][N]."""
+    as one fused kernel.  in_f32 [M][Kk] -> out_f32 [M][N]."""
     call("madi_q8_pproj", ptr(out_f32), ptr(in_f32), w.qs, w.scales, M, N, Kk)
+
+
+def proj(in16, in_f32, w16, out_f32, B: int, N: int, Kk: int) -> None:
+    """decoder.zig:337-341 (proj: kCvt32 + matmulF16Batched + kCvt16 on the
+    F16 copy w16 of a Q8 weight); in16 is the BScratch staging buffer.  A w16
+    that deqW16 recorded runs the fused batched projection on the Q8 weight."""
+    call("madi_proj_f16w", ptr(out_f32), ptr(in_f32), ptr(w16), ptr(in16), B, N, Kk)
 
 
 def kQkv(q_out, x, w: Q8, qb, vb, kc, vc, pos, d: int = D) -> None:
@@ -215,15 +245,23 @@ def embLookupIndirect(out, qs: int, sc: int, tokens, pos, vocab: int = VOCAB,
     call("madi_q8_emb_lookup_indirect", ptr(out), qs, sc, ptr(tokens), ptr(pos), vocab, dim)
 
 
+def prefillEmbed(out, qs: int, sc: int, tokens, pe, pos0: int, M: int, dim: int = D,
+                 vocab: int = VOCAB) -> None:
+    """decoder.zig:460-467 (emb_pe_rows_q8): out[m] = emb(tokens[m]) + pe[pos0 + m]
+    over the tied Q8 tok_emb; tokens a device u32 [M], pe a device f32 table."""
+    call("madi_q8_emb_pe_rows", ptr(out), qs, sc, ptr(tokens), ptr(pe), dim, pos0, M, vocab)
+
+
 def gemv_f16x(out, x16, w: Q8, n: int, k: int, bias=None, epilogue: int = EPI_NONE) -> None:
     """Q8 GEMV with fp16 activations (the measured decoder-GEMV configuration)."""
     call("madi_q8_gemv_f16x", ptr(out), ptr(x16), w.qs, w.scales, ptr(bias), n, k, epilogue)
 
 
 __all__ = [
-    "D", "MLP", "VOCAB", "ENC_SEQ", "Q8", "init", "sync", "repack_host", "unpack_host",
+    "D", "MLP", "VOCAB", "ENC_SEQ", "Q8", "init", "sync", "getFunction", "materialize",
+    "set_deferred_dequant", "repack_host", "unpack_host",
     "upload_q8", "upload_q8_device_repack", "quantize", "fnv", "FNV_SEED", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias", "kM4", "kM4Bias", "matmulF16Batched",
-    "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "pproj", "kQkv", "kLogitGemv", "embLookup",
-    "embLookupIndirect", "gemv_f16x", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU",
+    "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "pproj", "proj", "kQkv", "kLogitGemv", "embLookup",
+    "embLookupIndirect", "prefillEmbed", "gemv_f16x", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU",
     "EPI_BIAS_RES",
 ]

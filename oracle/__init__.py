@@ -57,6 +57,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "oracle_fnv1a64": (ctypes.c_uint64, [ctypes.c_uint64, _P, ctypes.c_size_t]),
         "oracle_fnv_q8": (ctypes.c_uint64, [ctypes.c_uint64, _P, ctypes.c_size_t, _P, ctypes.c_size_t]),
         "oracle_emb_row_q8": (None, [_P, _P, _P, _U32, _U32]),
+        "oracle_emb_pe_rows_q8": (None, [_P, _P, _P, _P, _P, _U32, _U32, _U32]),
         "oracle_gemm_f16": (None, [_P, _P, _P, _U32, _U32, _U32, ctypes.c_float, ctypes.c_float, _I]),
     }
     for name, (res, args) in sig.items():
@@ -200,6 +201,20 @@ def emb_row_q8(qs, scales, tok: int):
     out = np.empty(dim, dtype=np.float32)
     lib().oracle_emb_row_q8(_ptr(out), _ptr(_c(qs, np.int8)), _ptr(_c(scales, np.float16)),
                             tok, dim)
+    return out
+
+
+def emb_pe_rows_q8(qs, scales, tokens, pe, pos0: int):
+    """emb_pe_rows_q8 (decoder_ops.metal:614-633): [M][dim] f32 rows of the
+    natural-layout table at `tokens` plus rows pos0.. of `pe`."""
+    n, dim = _check_q8(qs, scales)
+    tokens = np.ascontiguousarray(tokens, dtype=np.uint32)
+    pe = np.ascontiguousarray(pe, dtype=np.float32)
+    m = tokens.size
+    assert np.all(tokens < n) and pe.shape[1] == dim and pos0 + m <= pe.shape[0]
+    out = np.empty((m, dim), dtype=np.float32)
+    lib().oracle_emb_pe_rows_q8(_ptr(out), _ptr(_c(qs, np.int8)), _ptr(_c(scales, np.float16)),
+                                _ptr(tokens), _ptr(pe), dim, pos0, m)
     return out
 
 

@@ -274,6 +274,20 @@ void oracle_emb_row_q8(float *out, const int8_t *qs, const uint16_t *scales, uin
   for (uint32_t d = 0; d < dim; ++d) out[d] = deq(qs, scales, dim, tok, d);
 }
 
+/* ---- Q8 embedding rows plus positions (sequence prefill) ------------------------
+ * engine/metal/kernels/decoder_ops.metal:614-633 (emb_pe_rows_q8):
+ *   out[m*dim + d] = float(qs[tokens[m]*dim + d]) * float(scales[tokens[m]*(dim/32) + d/32])
+ *                    + pe[(pos0 + m)*dim + d] */
+void oracle_emb_pe_rows_q8(float *out, const int8_t *qs, const uint16_t *scales,
+                           const uint32_t *tokens, const float *pe, uint32_t dim, uint32_t pos0,
+                           uint32_t m) {
+  for (uint32_t r = 0; r < m; ++r)
+    for (uint32_t d = 0; d < dim; ++d) {
+      const float e = deq(qs, scales, dim, tokens[r], d);
+      out[(size_t)r * dim + d] = e + pe[(size_t)(pos0 + r) * dim + d];
+    }
+}
+
 /* ---- f16 GEMM on pre-dequantised weights ---------------------------------------
  * The MPS op behind mtl_matmul_f16_enc (engine/metal/metal_backend.h:103):
  * C[M][N] = alpha * A[M][K] . B[K][N] + beta * C, all f16 row-major.  MPS does not

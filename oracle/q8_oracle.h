@@ -81,6 +81,11 @@ uint64_t oracle_fnv_q8(uint64_t seed, const int8_t *qs, size_t nq, const uint16_
 
 void oracle_emb_row_q8(float *out, const int8_t *qs, const uint16_t *scales, uint32_t tok,
                        uint32_t dim);
+/* decoder_ops.metal:614-633 emb_pe_rows_q8: rows tokens[0..m) of the natural-layout
+ * table plus positional rows pos0..pos0+m-1 of pe ([*][dim] f32). */
+void oracle_emb_pe_rows_q8(float *out, const int8_t *qs, const uint16_t *scales,
+                           const uint32_t *tokens, const float *pe, uint32_t dim, uint32_t pos0,
+                           uint32_t m);
 
 void oracle_gemm_f16(uint16_t *c, const uint16_t *a, const uint16_t *b, uint32_t m,
                      uint32_t n, uint32_t k, float alpha, float beta, int threads);

@@ -43,6 +43,25 @@ def test_header_compiles_as_c(tmp_path):
 
 FAKE = 0x100000  # 16-byte aligned, never dereferenced: every call below fails validation first
 
+HANDLE_NAMES = ["dequant_q8_f16", "m4_gemm_nn", "m4_gemm_bias", "m4_gemm_bias_gelu", "gemv_q8",
+                "gemv_q8_bias", "gemv_q8_bias_gelu", "gemv_q8_bias_res", "gemv_q8_qkv",
+                "logit_gemv_q8", "gpu_emb_lookup_q8", "emb_lookup_indirect_q8", "emb_pe_rows_q8",
+                "mul_mm_q8"]
+
+
+def test_function_handles_by_name():
+    """madi_get_function (mtl_get_function): one distinct handle per kernel name
+    of the path, an error for any other name; the handle-taking wrappers
+    refuse a handle of the wrong kind before touching a device."""
+    ids = {name: q8.getFunction(name) for name in HANDLE_NAMES}
+    assert len(set(ids.values())) == len(HANDLE_NAMES) and all(v > 0 for v in ids.values())
+    out = ctypes.c_int(-1)
+    assert madi_amd.lib().madi_get_function(b"layer_norm_f16", ctypes.byref(out)) == -9
+    L = madi_amd.lib()
+    assert L.madi_m4_gemm(ids["gemv_q8"], FAKE, FAKE, FAKE, None, 16, 256, 1280) == -9
+    assert L.madi_q8_gemv_epi(ids["m4_gemm_bias"], FAKE, FAKE, FAKE, FAKE, FAKE, 256, 1280) == -9
+    assert L.madi_m4_gemm(ids["m4_gemm_nn"], FAKE, FAKE, FAKE, None, 16, 256, 1280) == -8
+
 
 @pytest.mark.parametrize("call,args,code", [
     ("madi_q8_gemm", (FAKE, FAKE, FAKE, FAKE, None, 0, 256, 1280, 0), -5),        # m == 0
@@ -56,6 +75,10 @@ FAKE = 0x100000  # 16-byte aligned, never dereferenced: every call below fails v
     ("madi_q8_gemv", (FAKE, FAKE, FAKE, FAKE, 100, 96), -5),
     ("madi_q8_gemv", (FAKE, FAKE, FAKE + 8, FAKE, 100, 1280), -7),
     ("madi_q8_gemv", (FAKE, FAKE, FAKE, FAKE, 1 << 21, 1024), -5),                # 2 GiB weight
+    ("madi_q8_emb_pe_rows", (FAKE, FAKE, FAKE, FAKE, FAKE, 96, 0, 4, 100), -5),   # dim % 64
+    ("madi_q8_emb_pe_rows", (FAKE, FAKE, FAKE, None, FAKE, 1280, 0, 4, 100), -6), # null tokens
+    ("madi_q8_emb_pe_rows", (FAKE, FAKE, FAKE, FAKE, FAKE + 4, 1280, 0, 4, 100), -7),  # pe
+    ("madi_q8_emb_pe_rows", (FAKE, FAKE, FAKE, FAKE, FAKE, 1280, 0, 4, 100), -8),
     ("madi_q8_logit_gemv", (FAKE, FAKE, FAKE, FAKE, 1 << 22, 512), -5),           # 2 GiB vocab
     ("madi_q8_gemv", (FAKE, FAKE, FAKE, FAKE, 100, 1280), -8),
     ("madi_q8_gemv_bias", (FAKE, FAKE, FAKE, FAKE, None, 100, 1280), -6),

@@ -1,0 +1,296 @@
+"""The engine's call sequences, unchanged, through the C ABI.
+
+The encoder's forward pass (engine/metal/encoder.zig:262-301) dequantises
+every Q8 weight into a shared F16 scratch (kDeq -> s.wdq / s.wdq2) and
+multiplies by it through handles resolved by name (kM4 / kM4Bias with
+m4_gemm_nn, m4_gemm_bias, m4_gemm_bias_gelu).  The batched decoder keeps F16
+copies made by deqW16 and projects through them (proj, decoder.zig:337-341).
+These tests replay those sequences verbatim through the Python mirror of the
+wrappers and check that the fused Q8 kernels ran (the F16 scratch is never
+written: it still holds a NaN sentinel) with results matching the oracle, and
+that the deferred dequantisation is written out wherever anything could
+observe it."""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from madi_amd import _lib, synth
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+D, MLP, M = 1280, 5120, 1500
+NAN16 = np.uint16(0x7E00)
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def q():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    import madi_amd.q8 as q8
+    q8.init()
+    q8.set_deferred_dequant(True)
+    return q8
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def dev_f16(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float16).view(np.int16)).cuda()
+
+
+def host_f16(t):
+    return t.cpu().numpy().view(np.float16)
+
+
+def sentinel(n):
+    return torch.from_numpy(np.full(n, NAN16, np.uint16).view(np.int16)).cuda()
+
+
+def normwise(c, ref):
+    c = np.asarray(c, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return np.max(np.abs(c - ref)) / max(np.max(np.abs(ref)), 1e-30)
+
+
+ROWS = np.unique(np.r_[np.arange(0, M, 32), np.arange(31, M, 32), M - 1])
+
+
+def check_gemm(c16, a, qs, sc, bias=None, epi=O.EPI_NONE):
+    c = host_f16(c16)[ROWS].astype(np.float64)
+    ref = O.q8_gemm_rows(a, qs, sc, rows=ROWS, bias=bias, epilogue=epi, threads=16)
+    assert np.all(np.isfinite(c))
+    err = normwise(c, ref)
+    assert err <= TOL, err
+
+
+def test_encoder_layer_unchanged_sequence(q):
+    """One encoder layer's Q8 calls exactly as encoder.zig:262-301 issues them
+    on the tensor-op path (K.m4_bias, K.m4_nn, K.m4_bias_gelu all resolved):
+    q, k, v with bias from slices of the stacked q|k|v weight through s.wdq
+    and s.wdq2, out-proj, fc1 + bias + GELU, and fc2 on fc1's output.  The
+    attention and layer-norm kernels between them are not part of this path:
+    their outputs are synthetic here."""
+    say("encoder layer, unchanged call sequence")
+    rng = np.random.default_rng(262)
+    m4 = q.getFunction("m4_gemm_nn")
+    m4b = q.getFunction("m4_gemm_bias")
+    m4bg = q.getFunction("m4_gemm_bias_gelu")
+    qkv_qs, qkv_sc = synth.q8_weight(rng, 3 * D, D)
+    o_qs, o_sc = synth.q8_weight(rng, D, D)
+    m0_qs, m0_sc = synth.q8_weight(rng, MLP, D)
+    m2_qs, m2_sc = synth.q8_weight(rng, D, MLP)
+    qkv_w, o_w = q.upload_q8(qkv_qs, qkv_sc), q.upload_q8(o_qs, o_sc)
+    m0_w, m2_w = q.upload_q8(m0_qs, m0_sc), q.upload_q8(m2_qs, m2_sc)
+    q_b, k_b, v_b = (rng.standard_normal(D).astype(np.float32) for _ in range(3))
+    m0_b = rng.standard_normal(MLP).astype(np.float32)
+    x_ln = synth.activations(rng, M, D)     # layer norm output (kLN)
+    ao = synth.activations(rng, M, D)       # attention output (kFlash)
+    x_ln2 = synth.activations(rng, M, D)    # bias + residual + layer norm output (kBRLN)
+    wdq, wdq2 = sentinel(D * MLP), sentinel(D * MLP)   # Scratch.wdq / wdq2
+    d_x, d_ao, d_x2 = dev_f16(x_ln), dev_f16(ao), dev_f16(x_ln2)
+    qo, ko, vo, mo = (torch.empty((M, D), dtype=torch.int16, device="cuda") for _ in range(4))
+    mh = torch.empty((M, MLP), dtype=torch.int16, device="cuda")
+    mo2 = torch.empty((M, D), dtype=torch.int16, device="cuda")
+    d_qb, d_kb, d_vb, d_m0b = dev(q_b), dev(k_b), dev(v_b), dev(m0_b)
+
+    # encoder.zig:262-301, the K.m4_bias / K.m4_nn / K.m4_bias_gelu branches
+    q.kDeq(wdq, qkv_w, D, D)
+    q.kM4Bias(m4b, d_x, wdq, qo, d_qb, M, D, D)
+    q.kDeq(wdq2, qkv_w.rows(D, D), D, D)
+    q.kM4Bias(m4b, d_x, wdq2, ko, d_kb, M, D, D)
+    q.kDeq(wdq, qkv_w.rows(2 * D, D), D, D)
+    q.kM4Bias(m4b, d_x, wdq, vo, d_vb, M, D, D)
+    q.kDeq(wdq, o_w, D, D)
+    q.kM4(m4, d_ao, wdq, mo, M, D, D)
+    q.kDeq(wdq, m0_w, MLP, D)
+    q.kM4Bias(m4bg, d_x2, wdq, mh, d_m0b, M, MLP, D)
+    q.kDeq(wdq2, m2_w, D, MLP)
+    q.kM4(m4, mh, wdq2, mo2, M, D, MLP)
+    q.sync()
+
+    # the F16 scratch was never written: every product ran the fused Q8 GEMM
+    assert np.all(wdq.cpu().numpy().view(np.uint16) == NAN16)
+    assert np.all(wdq2.cpu().numpy().view(np.uint16) == NAN16)
+    check_gemm(qo, x_ln, qkv_qs[:D], qkv_sc[:D], q_b, O.EPI_BIAS)
+    check_gemm(ko, x_ln, qkv_qs[D:2 * D], qkv_sc[D:2 * D], k_b, O.EPI_BIAS)
+    check_gemm(vo, x_ln, qkv_qs[2 * D:], qkv_sc[2 * D:], v_b, O.EPI_BIAS)
+    check_gemm(mo, ao, o_qs, o_sc)
+    check_gemm(mh, x_ln2, m0_qs, m0_sc, m0_b, O.EPI_BIAS_GELU)
+    check_gemm(mo2, host_f16(mh), m2_qs, m2_sc)   # fc2 consumes the GPU's fc1 output
+
+    # anything that reads the scratch now sees the dequantised weights: the
+    # last kDeq into each buffer (fc1 -> wdq, fc2 -> wdq2), bit for bit
+    q.materialize(None)
+    q.sync()
+    assert np.array_equal(wdq.cpu().numpy().view(np.uint16),
+                          O.dequant_q8_f16(m0_qs, m0_sc).view(np.uint16).reshape(-1))
+    assert np.array_equal(wdq2.cpu().numpy().view(np.uint16),
+                          O.dequant_q8_f16(m2_qs, m2_sc).view(np.uint16).reshape(-1))
+
+
+def test_encoder_sequence_without_deferral(q):
+    """The same pairs with the deferral off: kDeq writes the F16 scratch and
+    kM4 / kM4Bias run the library F16 GEMM with the reference's rounding
+    order (product rounded to f16, then bias).  Same results to the gate."""
+    say("encoder pairs, deferral off")
+    rng = np.random.default_rng(263)
+    m = 257
+    qs, sc = synth.q8_weight(rng, MLP, D)
+    w = q.upload_q8(qs, sc)
+    bias = rng.standard_normal(MLP).astype(np.float32)
+    a = synth.activations(rng, m, D)
+    wdq = sentinel(D * MLP)
+    c = torch.empty((m, MLP), dtype=torch.int16, device="cuda")
+    q.set_deferred_dequant(False)
+    try:
+        q.kDeq(wdq, w, MLP, D)
+        q.kM4Bias("m4_gemm_bias_gelu", dev_f16(a), wdq, c, dev(bias), m, MLP, D)
+        q.sync()
+    finally:
+        q.set_deferred_dequant(True)
+    assert np.array_equal(wdq.cpu().numpy().view(np.uint16),
+                          O.dequant_q8_f16(qs, sc).view(np.uint16).reshape(-1))
+    got = host_f16(c).astype(np.float64)
+    ref = O.q8_gemm_rows(a, qs, sc, bias=bias, epilogue=O.EPI_BIAS_GELU, threads=16)
+    assert normwise(got, ref) <= TOL
+
+
+def test_decoder_handles_and_proj(q):
+    """decoder.zig: kGemvQ8BiasEpi with the handles of gemv_q8_bias_gelu and
+    gemv_q8_bias_res gives the dedicated entry points' results bit for bit;
+    proj on deqW16's F16 copies (decoder.zig:337-341) runs the batched
+    projection from the Q8 weight (equal to pproj, copies never written), and
+    on a true F16 weight the library GEMM (to the gate)."""
+    say("decoder handles and proj")
+    rng = np.random.default_rng(337)
+    qs, sc = synth.q8_weight(rng, MLP, D)
+    w = q.upload_q8(qs, sc)
+    x = dev(rng.standard_normal(D).astype(np.float32))
+    bias = dev(rng.standard_normal(MLP).astype(np.float32))
+    res0 = rng.standard_normal(MLP).astype(np.float32)
+    for name, direct in (("gemv_q8_bias_gelu", "madi_q8_gemv_bias_gelu"),
+                         ("gemv_q8_bias_res", "madi_q8_gemv_bias_res")):
+        o1, o2 = dev(res0.copy()), dev(res0.copy())
+        q.kGemvQ8BiasEpi(q.getFunction(name), o1, x, w, bias, MLP, D)
+        _lib.call(direct, o2.data_ptr(), x.data_ptr(), w.qs, w.scales, bias.data_ptr(), MLP, D)
+        q.sync()
+        assert torch.equal(o1, o2), name
+
+    B = 8
+    wf16 = sentinel(D * MLP)                  # WF16.m0w, [D][MLP]
+    in16 = torch.empty(B * MLP, dtype=torch.int16, device="cuda")   # BScratch.in16
+    xin = rng.standard_normal((B, D)).astype(np.float32)
+    q.deqW16(wf16, w, MLP, D)
+    out = torch.empty((B, MLP), dtype=torch.float32, device="cuda")
+    q.proj(in16, dev(xin), wf16, out, B, MLP, D)
+    want = torch.empty((B, MLP), dtype=torch.float32, device="cuda")
+    q.pproj(dev(xin), w, want, B, MLP, D)
+    q.sync()
+    assert torch.equal(out, want)
+    assert np.all(wf16.cpu().numpy().view(np.uint16) == NAN16)
+    # a true F16 weight (not recorded): f16 staging + library GEMM, f32 out
+    w16 = dev_f16(O.dequant_q8_f16(qs, sc))
+    out2 = torch.empty((B, MLP), dtype=torch.float32, device="cuda")
+    q.proj(in16, dev(xin), w16, out2, B, MLP, D)
+    q.sync()
+    assert normwise(out2.cpu().numpy(), O.q8_proj(xin, qs, sc, threads=8)) <= TOL
+
+
+class DevBuf:
+    """A madi_alloc buffer (the library sees its extent)."""
+
+    def __init__(self, nbytes):
+        self.n = nbytes
+        self.p = _lib.lib().madi_alloc(nbytes)
+        assert self.p
+
+    def up(self, arr):
+        arr = np.ascontiguousarray(arr)
+        _lib.call("madi_upload", self.p, arr.ctypes.data, arr.nbytes)
+
+    def down(self, dtype, count):
+        out = np.empty(count, dtype)
+        _lib.call("madi_download", out.ctypes.data, self.p, out.nbytes)
+        return out
+
+    def free(self):
+        _lib.lib().madi_free(self.p)
+        self.p = None
+
+
+def q8_devbufs(q, qs, sc):
+    tq, ts = q.repack_host(qs, sc)
+    bq, bs = DevBuf(tq.nbytes), DevBuf(ts.nbytes)
+    bq.up(tq)
+    bs.up(ts)
+    return bq, bs
+
+
+def test_deferred_dequant_is_written_when_observable(q):
+    """A recorded kDeq is carried out before anything could see the
+    difference: a download of wdq, an upload into the Q8 source, a madi_free
+    of the source, a partial overwrite of wdq; a full overwrite drops it."""
+    say("deferred dequantisation triggers")
+    rng = np.random.default_rng(429)
+    n, k = 96, 256
+    qs, sc = synth.q8_weight(rng, n, k)
+    qs2, sc2 = synth.q8_weight(rng, n, k)
+    want = O.dequant_q8_f16(qs, sc).view(np.uint16).reshape(-1)
+    nw = n * k
+    wdq = DevBuf(nw * 2)
+    bq, bs = q8_devbufs(q, qs, sc)
+
+    def fresh_sentinel():
+        wdq.up(np.full(nw, NAN16, np.uint16))
+
+    # 1. download of wdq
+    fresh_sentinel()
+    _lib.call("madi_q8_dequant_f16", wdq.p, bq.p, bs.p, n, k)
+    assert np.array_equal(wdq.down(np.uint16, nw), want)
+    # 2. an upload into the Q8 source: wdq keeps the weights it was made from
+    fresh_sentinel()
+    _lib.call("madi_q8_dequant_f16", wdq.p, bq.p, bs.p, n, k)
+    tq2, ts2 = q.repack_host(qs2, sc2)
+    bq.up(tq2)
+    bs.up(ts2)
+    assert np.array_equal(wdq.down(np.uint16, nw), want)
+    # 3. madi_free of the source
+    fresh_sentinel()
+    bq.up(q.repack_host(qs, sc)[0])
+    bs.up(q.repack_host(qs, sc)[1])
+    _lib.call("madi_q8_dequant_f16", wdq.p, bq.p, bs.p, n, k)
+    bq.free()
+    bs.free()
+    assert np.array_equal(wdq.down(np.uint16, nw), want)
+    # 4. a partial overwrite of wdq lands on top of the dequantised weights
+    bq, bs = q8_devbufs(q, qs, sc)
+    fresh_sentinel()
+    _lib.call("madi_q8_dequant_f16", wdq.p, bq.p, bs.p, n, k)
+    head = np.arange(8, dtype=np.uint16)
+    wdq.up(head)
+    got = wdq.down(np.uint16, nw)
+    assert np.array_equal(got[:8], head) and np.array_equal(got[8:], want[8:])
+    # 5. a full overwrite drops the record: a GEMM on wdq multiplies the new data
+    _lib.call("madi_q8_dequant_f16", wdq.p, bq.p, bs.p, n, k)
+    w16 = (rng.standard_normal((k, n)) * 0.01).astype(np.float16)
+    wdq.up(w16.view(np.uint16))
+    a = synth.activations(rng, 40, k)
+    c = torch.empty((40, n), dtype=torch.int16, device="cuda")
+    q.kM4("m4_gemm_nn", dev_f16(a), wdq.p, c, 40, n, k)
+    q.sync()
+    ref = a.astype(np.float64) @ w16.astype(np.float64)
+    assert normwise(host_f16(c), ref) <= TOL
+    for b in (wdq, bq, bs):
+        b.free()

@@ -124,6 +124,7 @@ def test_dequant_bit_exact(q, n, k):
     w = q.upload_q8(qs, sc)
     out = torch.empty((k, n), dtype=torch.int16, device="cuda")
     q.kDeq(out, w, n, k)
+    q.materialize(out)  # torch reads wdq: the deferred dequantisation runs now
     q.sync()
     ref = O.dequant_q8_f16(qs, sc)
     assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
@@ -138,6 +139,7 @@ def test_stacked_row_slices(q):
     for blk in range(3):
         out = torch.empty((d, d), dtype=torch.int16, device="cuda")
         q.kDeq(out, w.rows(blk * d, d), d, d)
+        q.materialize(out)
         q.sync()
         ref = O.dequant_q8_f16(qs[blk * d:(blk + 1) * d], sc[blk * d:(blk + 1) * d])
         assert np.array_equal(out.cpu().numpy().view(np.uint16), ref.view(np.uint16))
@@ -261,10 +263,19 @@ def test_gemm_bias_epilogues(q, gelu, m, n):
     assert np.all(np.isfinite(c))
 
 
-@pytest.mark.parametrize("name,n,k", [("fc1", 5120, 1280), ("fc2", 1280, 5120), ("qkv", 3840, 1280)])
+# Every encoder and cross-attention projection at M = 1500 (one 30 s window)
+# and the kernel instance it runs on a 256-CU device: fc1 128-row tiles (240),
+# q|k|v 96-row tiles (240), cross K|V 64-row tiles (240), out-proj 32-row
+# tiles (235), fc2 64-row tiles (120) x 2 K splits of 40 chunks; all K loops
+# unpadded (20 or 40 chunks per workgroup).
+ENCODER_SHAPES = [("fc1", 5120, 1280), ("fc2", 1280, 5120), ("qkv", 3840, 1280),
+                  ("out", 1280, 1280), ("cross_kv", 2560, 1280)]
+
+
+@pytest.mark.parametrize("name,n,k", ENCODER_SHAPES)
 def test_gemm_encoder_shapes_full_m(q, name, n, k):
-    """M = 1500 (one 30 s window); the oracle checks a row sample that covers
-    every M-tile boundary and the tail."""
+    """M = 1500; the oracle checks a row sample that covers every M-tile
+    boundary and the tail, normwise and element-wise."""
     say(f"gemm encoder {name} m=1500 n={n} k={k}")
     m = 1500
     a, qs, sc = synth.gemm_case(0, m, n, k)
@@ -272,6 +283,47 @@ def test_gemm_encoder_shapes_full_m(q, name, n, k):
     rows = np.unique(np.r_[tile_rows(m), 1, 129, 1498])  # every 32-row tile boundary
     ref = O.q8_gemm_rows(a, qs, sc, rows=rows, threads=16)
     assert normwise(c[rows], ref) <= TOL
+    assert tight_ok(c[rows], a[rows], qs, sc)
+    assert np.all(np.isfinite(c))
+
+
+@pytest.mark.parametrize("name,n,k,gelu", [("fc1", 5120, 1280, True), ("fc2", 1280, 5120, False),
+                                           ("qkv", 3840, 1280, False), ("out", 1280, 1280, False)])
+def test_gemm_encoder_epilogues_full_m(q, name, n, k, gelu):
+    """The encoder's production epilogue instances at M = 1500: fc1 + bias +
+    GELU on 128-row tiles with an unpadded 20-chunk loop, fc2 + bias where the
+    two K splits meet in the last workgroup before the bias, q|k|v + bias on
+    96-row and out + bias on 32-row tiles (encoder.zig:262-301)."""
+    say(f"gemm encoder epilogue {name} m=1500 n={n} k={k} gelu={gelu}")
+    m = 1500
+    a, qs, sc = synth.gemm_case(5, m, n, k)
+    bias = np.random.default_rng(n + k).standard_normal(n).astype(np.float32)
+    ref_rows = np.unique(np.r_[tile_rows(m), 1, 129, 1498])
+    for rep in range(2 if name == "fc2" else 1):  # split K: the counters must return to zero
+        c = _gemm(q, a, qs, sc, bias=bias, gelu=gelu)
+        ref = O.q8_gemm_rows(a, qs, sc, rows=ref_rows, bias=bias,
+                             epilogue=O.EPI_BIAS_GELU if gelu else O.EPI_BIAS, threads=16)
+        assert normwise(c[ref_rows], ref) <= TOL, rep
+        assert tight_epi_ok(c[ref_rows], a[ref_rows], qs, sc, bias, gelu), rep
+        assert np.all(np.isfinite(c))
+
+
+@pytest.mark.parametrize("name,n,k", [("fc1", 5120, 1280), ("fc2", 1280, 5120)])
+def test_gemm_long_audio_full_m(q, name, n, k):
+    """16 stacked windows, M = 24000: 128-row tiles, 188 x 20 (fc1) and 188 x 5
+    (fc2) of them, several per CU; fc2's 80-chunk K runs unsplit and
+    unpadded.  Row sample over tile boundaries, the tail and random rows."""
+    say(f"gemm long audio {name} m=24000 n={n} k={k}")
+    m = 24000
+    rng = np.random.default_rng(24000 + n)
+    a = synth.activations(rng, m, k)
+    qs, sc = synth.q8_weight(rng, n, k)
+    c = _gemm(q, a, qs, sc)
+    rows = np.unique(np.r_[0, 31, 32, 127, 128, 255, 256, 12031, 12032, 23935, 23936,
+                           23967, 23968, 23999, rng.integers(0, m, 24)])
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, threads=16)
+    assert normwise(c[rows], ref) <= TOL
+    assert tight_ok(c[rows], a[rows], qs, sc)
     assert np.all(np.isfinite(c))
 
 
@@ -419,6 +471,35 @@ def test_emb_lookup_rows(q):
     assert np.array_equal(out.cpu().numpy(), O.emb_row_q8(qs, sc, 51864))
 
 
+@pytest.mark.parametrize("m,pos0", [(1, 0), (4, 7), (37, 100), (320, 128)])
+def test_emb_pe_rows(q, m, pos0):
+    """Sequence prefill's embedding (emb_pe_rows_q8 behind prefillEmbed) from
+    the panel-layout tied tok_emb, bit-exact against the oracle: tokens from
+    every part of the vocab including the 26-row last panel; an
+    out-of-vocab token leaves its row untouched."""
+    n, k = 51866, 1280
+    say(f"emb_pe_rows m={m} pos0={pos0}")
+    rng = np.random.default_rng(m + pos0)
+    qs, sc = synth.q8_weight(rng, n, k)
+    w = q.upload_q8(qs, sc)
+    toks = rng.integers(0, n, m).astype(np.uint32)
+    toks[: min(m, 4)] = np.array([0, 51865, 51840, 31], np.uint32)[: min(m, 4)]
+    pe = rng.standard_normal((448, k)).astype(np.float32)
+    out = torch.full((m, k), 7.0, dtype=torch.float32, device="cuda")
+    tt = toks.copy()
+    if m > 4:
+        tt[4] = n  # out of range: row stays at 7.0
+    q.prefillEmbed(out, w.qs, w.scales, dev(tt.view(np.int32)), dev(pe), pos0, m, k, n)
+    q.sync()
+    got = out.cpu().numpy()
+    ref = O.emb_pe_rows_q8(qs, sc, toks, pe, pos0)
+    keep = np.ones(m, bool)
+    if m > 4:
+        keep[4] = False
+        assert np.all(got[4] == 7.0)
+    assert np.array_equal(got[keep], ref[keep])
+
+
 # ------------------------------------------------------------------ batched / skinny projection
 def _pproj(q, x, qs, sc):
     m, k = x.shape
@@ -447,6 +528,9 @@ def staged_ok(c, x, qs, sc):
     (32, 1280, 1280), (33, 3840, 1280), (70, 1280, 5120), (5, 40, 64),
     (17, 5120, 1280),    # one 32-row slice, 15 rows past M
     (320, 1280, 1280),   # sequence prefill at its largest M: ten slices
+    # the batched decode step at M = 16: vocab (four-panel groups, tail panel),
+    # q|k|v, FFN up and the 1280 x 1280 projections (single panels, unsplit)
+    (16, 51866, 1280), (16, 3840, 1280), (16, 5120, 1280), (16, 1280, 1280),
 ])
 def test_pproj_parity(q, m, n, k):
     say(f"pproj m={m} n={n} k={k}")
@@ -666,9 +750,10 @@ def test_f16_gemm_kM4_epilogues(q, epi):
     bias = np.random.default_rng(78).standard_normal(n).astype(np.float32)
     dc = torch.empty((m, n), dtype=torch.int16, device="cuda")
     if epi == O.EPI_NONE:
-        q.kM4(dev_f16(a), dev_f16(w16), dc, m, n, k)
+        q.kM4("m4_gemm_nn", dev_f16(a), dev_f16(w16), dc, m, n, k)
     else:
-        q.kM4Bias(dev_f16(a), dev_f16(w16), dc, dev(bias), m, n, k, gelu=epi == O.EPI_BIAS_GELU)
+        q.kM4Bias("m4_gemm_bias_gelu" if epi == O.EPI_BIAS_GELU else "m4_gemm_bias",
+                  dev_f16(a), dev_f16(w16), dc, dev(bias), m, n, k)
     q.sync()
     got = host_f16(dc).astype(np.float64)
     c16 = O.gemm_f16(a, w16, threads=8)

@@ -323,6 +323,23 @@ def test_emb_row_is_f32_dequant():
     assert np.array_equal(row, ref)
 
 
+def test_emb_pe_rows_is_row_plus_position():
+    """emb_pe_rows_q8 = the f32 dequantised row (exact: 8 x 11 significant
+    bits) plus the positional row, one f32 rounding; with zero positions it
+    is the embedding row itself, with zero quants the positional row."""
+    rng = np.random.default_rng(23)
+    qs, sc = _q8(rng, 12, 128)
+    pe = rng.standard_normal((40, 128)).astype(np.float32)
+    toks = np.array([3, 0, 11, 3, 7], np.uint32)
+    got = O.emb_pe_rows_q8(qs, sc, toks, pe, 30)
+    for m, t in enumerate(toks):
+        row = qs[t].astype(np.float64) * np.repeat(sc[t].astype(np.float64), 32)
+        assert np.array_equal(got[m], (row + pe[30 + m].astype(np.float64)).astype(np.float32))
+    assert np.array_equal(O.emb_pe_rows_q8(qs, sc, toks, np.zeros_like(pe), 30)[2],
+                          O.emb_row_q8(qs, sc, 11))
+    assert np.array_equal(O.emb_pe_rows_q8(np.zeros_like(qs), sc, toks, pe, 1), pe[1:6])
+
+
 def test_gemm_f16_alpha_beta():
     rng = np.random.default_rng(20)
     m, n, k = 9, 24, 40
