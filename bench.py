@@ -68,42 +68,68 @@ def gemv_bytes():
     return VOCAB * DIM + VOCAB * (DIM // 32) * 2 + DIM * 2 + VOCAB * 4
 
 
-def cpu_baseline(threads: int):
+def cpu_share() -> int:
+    """Host threads the CPU baseline may use: the CPUs this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets it (a one-GPU share
+    of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        n = min(n, int(env))
+    return max(1, n)
+
+
+def _median_time(fn, runs: int) -> float:
+    fn()  # warm-up
+    ts = []
+    for _ in range(runs):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return float(np.median(ts))
+
+
+def cpu_baseline(threads: int, runs: int = 5):
     """The oracle (C restatement of the reference's CPU loop,
-    engine/metal/test_q8gemm.zig:59-69) on a bounded row sample of the same
-    fc1 workload, and the vocab GEMV in full; single thread and `threads`."""
+    engine/metal/test_q8gemm.zig:59-69: dequantise to fp32, k-sequential fp32
+    accumulation) built for this host (-O3 -march=native, no BLAS), on the
+    same fc1 and vocab workloads: (i) the literal single-thread loop on a
+    96-row sample of fc1 (rows are independent: the rate per row is the
+    rate) and the full vocab GEMV, (ii) OpenMP over output rows on `threads`
+    threads for all 1500 rows and the vocab GEMV; each the median of `runs`
+    runs after one warm-up."""
+    import tempfile
     import oracle as O
     from madi_amd import synth
+    build = "prebuilt -O3 -march=x86-64-v3 (no compiler on this host)"
+    native = O.build_native(tempfile.mkdtemp(prefix="madi_oracle_"))
+    if native:
+        O.use_library(native)
+        build = "-O3 -march=native -ffp-contract=off -fopenmp (built here)"
     a, qs, sc = synth.gemm_case(0, M, N, K)
-    res = {}
-    rows1 = np.arange(0, M, 3, dtype=np.uint32)[:480]
-    O.q8_gemm_rows(a, qs, sc, rows=rows1[:2], threads=1)  # warm-up
-    t = time.perf_counter()
-    O.q8_gemm_rows(a, qs, sc, rows=rows1, threads=1)
-    dt1 = time.perf_counter() - t
+    rows1 = np.arange(0, M, M // 96, dtype=np.uint32)[:96]
     rowsn = np.arange(0, M, dtype=np.uint32)
-    t = time.perf_counter()
-    O.q8_gemm_rows(a, qs, sc, rows=rowsn, threads=threads)
-    dtn = time.perf_counter() - t
     f_row = 2.0 * N * K
-    res["gemm_1t_tflops"] = f_row * rows1.size / dt1 / 1e12
-    res["gemm_nt_tflops"] = f_row * rowsn.size / dtn / 1e12
+    dt1 = _median_time(lambda: O.q8_gemm_rows(a, qs, sc, rows=rows1, threads=1), runs)
+    dtn = _median_time(lambda: O.q8_gemm_rows(a, qs, sc, rows=rowsn, threads=threads), runs)
     x, qv, sv = synth.gemv_case(0, VOCAB, DIM)
     xf = x.astype(np.float32)
-    t = time.perf_counter()
-    for _ in range(3):
-        O.q8_gemv(xf, qv, sv, threads=1)
-    dtv1 = (time.perf_counter() - t) / 3
-    t = time.perf_counter()
-    for _ in range(10):
-        O.q8_gemv(xf, qv, sv, threads=threads)
-    dtvn = (time.perf_counter() - t) / 10
-    res["gemv_1t_gbs"] = gemv_bytes() / dtv1 / 1e9
-    res["gemv_nt_gbs"] = gemv_bytes() / dtvn / 1e9
-    res["sample"] = (f"fc1 GEMM: {rows1.size} of {M} rows single-thread ({dt1:.1f} s, rate per row) "
-                     f"and all {rowsn.size} rows on {threads} threads ({dtn:.1f} s); vocab GEMV: "
-                     f"full 1x{DIM}x{VOCAB}, 3 runs single-thread, 10 on {threads} threads")
-    return res
+    dtv1 = _median_time(lambda: O.q8_gemv(xf, qv, sv, threads=1), runs)
+    dtvn = _median_time(lambda: O.q8_gemv(xf, qv, sv, threads=threads), runs)
+    return {
+        "gemm_1t_tflops": f_row * rows1.size / dt1 / 1e12,
+        "gemm_nt_tflops": f_row * rowsn.size / dtn / 1e12,
+        "gemv_1t_gbs": gemv_bytes() / dtv1 / 1e9,
+        "gemv_nt_gbs": gemv_bytes() / dtvn / 1e9,
+        "build": build,
+        "sample": (f"fc1 GEMM: {rows1.size} of {M} rows on 1 thread ({dt1:.2f} s per run) and all "
+                   f"{rowsn.size} rows on {threads} threads ({dtn:.2f} s); vocab GEMV 1x{DIM}x{VOCAB} "
+                   f"in full on 1 ({dtv1:.3f} s) and {threads} threads ({dtvn:.3f} s); median of "
+                   f"{runs} runs after a warm-up each"),
+    }
 
 
 # ---------------------------------------------------------------- other configurations
@@ -212,27 +238,8 @@ def config_batched_decode(torch, stream, q8, reps=20):
         t = _timed(torch, stream, step, reps)
         byts = step_bytes + DEC_LAYERS * sum(m * k * 4 + m * n * 4 for _, n, k in DEC_SHAPES) \
             + m * DIM * 4 + m * VOCAB * 4
-        # the same step captured once per weight set into a HIP graph and
-        # replayed: the 25 launches no longer wait on the host
-        graphs = []
-        side = torch.cuda.Stream()
-        side.wait_stream(stream)
-        for s_ in range(2):
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.stream(side):
-                with torch.cuda.graph(g, stream=side):
-                    q8.init(side)
-                    step(s_)
-            graphs.append(g)
-        q8.init(stream)
-        torch.cuda.synchronize()
-        tg = _timed(torch, stream, lambda i: graphs[i % 2].replay(), reps)
         res[f"m{m}"] = {"us_per_step": round(t * 1e6, 2), "gbs": round(byts / t / 1e9, 1),
-                        "frac_hbm_peak": round(byts / t / 1e9 / PEAK_HBM_GBS, 4),
-                        "us_per_step_graph": round(tg * 1e6, 2),
-                        "gbs_graph": round(byts / tg / 1e9, 1),
-                        "frac_hbm_peak_graph": round(byts / tg / 1e9 / PEAK_HBM_GBS, 4)}
-        del graphs
+                        "frac_hbm_peak": round(byts / t / 1e9 / PEAK_HBM_GBS, 4)}
         tv = _timed(torch, stream, lambda i, m=m: q8.pproj(xin, sets[i % 2][1], out, m, VOCAB, DIM),
                     reps)
         vb = VOCAB * DIM + VOCAB * (DIM // 32) * 2 + m * DIM * 4 + m * VOCAB * 4
@@ -293,29 +300,13 @@ def config_decode_token(torch, stream, q8, reps=20):
     token(0)
     token(1)
     t = _timed(torch, stream, token, reps)
-    graphs = []
-    side = torch.cuda.Stream()
-    side.wait_stream(stream)
-    for s_ in range(2):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.stream(side):
-            with torch.cuda.graph(g, stream=side):
-                q8.init(side)
-                token(s_)
-        graphs.append(g)
-    q8.init(stream)
-    torch.cuda.synchronize()
-    tg = _timed(torch, stream, lambda i: graphs[i % 2].replay(), reps)
-    del graphs
     res = {"workload": "decoder token at M = 1: 4 layers x (q|k|v + K/V store 1280->3840, out, "
                        "cross-q + bias, cross-out 1280->1280, FFN-up + bias + GELU 1280->5120, "
                        "FFN-down + bias + residual 5120->1280) + vocab logits 1280->51866, GEMV "
                        "family, f32 activations, weights cold (two alternating sets)",
            "weight_bytes_per_token": step_bytes,
            "us_per_token": round(t * 1e6, 2), "gbs": round(step_bytes / t / 1e9, 1),
-           "frac_hbm_peak": round(step_bytes / t / 1e9 / PEAK_HBM_GBS, 4),
-           "us_per_token_graph": round(tg * 1e6, 2),
-           "frac_hbm_peak_graph": round(step_bytes / tg / 1e9 / PEAK_HBM_GBS, 4)}
+           "frac_hbm_peak": round(step_bytes / t / 1e9 / PEAK_HBM_GBS, 4)}
     del sets
     base = _upload_layer(q8, 4990, 3 * d, d)
     ws = []
@@ -432,6 +423,11 @@ def main():
     def gemv(i):
         q8.gemv_f16x(dlog, dx, wv[i % GEMV_COPIES], VOCAB, DIM)
 
+    dx32 = torch.from_numpy(x16.astype(np.float32)).cuda()
+
+    def logit(i):  # the engine's kLogitGemv: f32 activations (transcribe.zig:4369)
+        q8.kLogitGemv(dlog, wv[i % GEMV_COPIES].qs, wv[i % GEMV_COPIES].scales, dx32, VOCAB, DIM)
+
     log(f"warmup {args.warmup} steps")
     for i in range(args.warmup):
         gemm(i)
@@ -453,12 +449,17 @@ def main():
     wall = time.perf_counter() - t0
     g_avg = ev[0].elapsed_time(ev[1]) * 1e-3 / args.steps   # s per GEMM launch
     v_avg = ev[1].elapsed_time(ev[2]) * 1e-3 / args.steps   # s per GEMV launch
+    for i in range(args.warmup):
+        logit(i)
+    l_avg = _timed(torch, stream, logit, args.steps)           # s per f32-x GEMV launch
+    l_gbs = (gemv_bytes() + DIM * 2) / l_avg / 1e9              # x is f32: 2 more bytes per element
     gemm_tflops = gemm_flops() / g_avg / 1e12
     gemv_gbs = gemv_bytes() / v_avg / 1e9
     ms_per_step = wall / args.steps * 1e3
     traffic = measured_traffic()
     log(f"gemm {g_avg*1e6:.2f} us ({gemm_tflops:.1f} TFLOP/s), gemv {v_avg*1e6:.2f} us "
-        f"({gemv_gbs:.0f} GB/s), wall {ms_per_step:.3f} ms/step")
+        f"({gemv_gbs:.0f} GB/s), f32-x gemv {l_avg*1e6:.2f} us ({l_gbs:.0f} GB/s), "
+        f"wall {ms_per_step:.3f} ms/step")
 
     result = {
         "metric": "Q8 GEMM TFLOP/s @1500x1280x5120 + Q8 GEMV GB/s @vocab; % of roofline",
@@ -494,6 +495,12 @@ def main():
                 "avg_us": round(v_avg * 1e6, 3),
                 "algorithmic_per_launch": gemv_bytes(),
             },
+            "engine_f32x": {
+                "what": "kLogitGemv as the engine calls it (f32 activations, "
+                        "madi_q8_logit_gemv), same cold rotation",
+                "avg_us": round(l_avg * 1e6, 3), "gbs": round(l_gbs, 1),
+                "frac": round(l_gbs / PEAK_HBM_GBS, 4),
+            },
         },
     }
     if not args.no_configs:
@@ -507,12 +514,14 @@ def main():
         cfg["long_audio"] = config_long_audio(torch, stream, q8)
         result["configs"] = cfg
     if not args.no_cpu:
-        threads = min(16, os.cpu_count() or 1)
-        log(f"cpu baseline on {threads} threads ({cpu_model()})")
+        threads = cpu_share()
+        log(f"cpu baseline on {threads} threads ({cpu_model()}, nproc {os.cpu_count()})")
         cb = cpu_baseline(threads)
         result["cpu_baseline"] = {
             "value": round(cb["gemm_nt_tflops"], 6), "unit": "TFLOP/s", "cores": threads,
             "kind": "port", "sample": cb["sample"], "cpu": cpu_model(),
+            "nproc": os.cpu_count(), "runs": 5, "median": True, "build": cb["build"],
+            "label": "reference CPU path (restated), baseline only",
             "single_thread": {"value": round(cb["gemm_1t_tflops"], 6), "unit": "TFLOP/s",
                               "cores": 1},
             "gemv": {"value": round(cb["gemv_nt_gbs"], 2), "unit": "GB/s", "cores": threads,

@@ -37,6 +37,30 @@ def lib() -> ctypes.CDLL:
     return _lib
 
 
+NATIVE_FLAGS = ["-O3", "-march=native", "-ffp-contract=off", "-fno-fast-math", "-fopenmp",
+                "-fPIC", "-shared"]
+
+
+def build_native(out_dir: str) -> str | None:
+    """Compile q8_oracle.c for the host it runs on (-march=native, the same
+    -ffp-contract=off arithmetic) into out_dir; returns the library path, or
+    None when no C compiler is available."""
+    out = os.path.join(out_dir, "libq8_oracle_native.so")
+    cc = os.environ.get("CC", "gcc")
+    r = subprocess.run([cc, *NATIVE_FLAGS, "-o", out, os.path.join(_HERE, "q8_oracle.c"), "-lm"],
+                       capture_output=True, text=True)
+    return out if r.returncode == 0 and os.path.exists(out) else None
+
+
+def use_library(path: str) -> None:
+    """Load the oracle functions from another build of q8_oracle.c (e.g. the
+    -march=native build of build_native)."""
+    global _lib
+    L = ctypes.CDLL(path)
+    _declare(L)
+    _lib = L
+
+
 _P = ctypes.c_void_p
 _U32 = ctypes.c_uint32
 _I = ctypes.c_int
