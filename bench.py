@@ -21,8 +21,8 @@ Beside the headline, "configs" reports the other measured workloads: the
 encoder GEMM set of one 30 s window (32 layers, independent weights), a
 batched decode step at M = 8 and 16 (skinny Q8 projections, cold weights) with
 the per-chunk cross-attention K|V GEMM, one decoder token at M = 1 through the
-GEMV family (and its fused q|k|v GEMV alone), and the 16-window long-audio
-fc1/fc2.
+GEMV family (and its fused q|k|v GEMV alone), one decoder layer's sequence
+prefill projections at M = 320, and the 16-window long-audio fc1/fc2.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-configs]
        python bench.py --calibrate-copy   (a plain 256 MiB device copy, the
@@ -321,6 +321,39 @@ def config_decode_token(torch, stream, q8, reps=20):
     return res
 
 
+def config_prefill(torch, stream, q8, reps=24):
+    """Sequence prefill at its largest M = 320 rows (prefillBlock,
+    decoder.zig:473-495): one decoder layer's pproj calls, q|k|v 1280->3840,
+    out, cross-q, cross-out 1280->1280, FFN 1280->5120->1280, f32 rows in and
+    out; weights cold (24 rotating copies of each)."""
+    from madi_amd import synth
+    m = 320
+    res = {"workload": "sequence prefill M=320: one decoder layer's batched projections "
+                       "(pproj: q|k|v 1280->3840, out, cross-q, cross-out 1280->1280, FFN "
+                       "1280->5120->1280), f32 in/out, cold weights"}
+    total = 0.0
+    flops = 0.0
+    for name, n, k in (("qkv", 3840, 1280), ("out", 1280, 1280), ("cross_q", 1280, 1280),
+                       ("cross_out", 1280, 1280), ("ffn_up", 5120, 1280), ("ffn_down", 1280, 5120)):
+        base = _upload_layer(q8, 5000 + n + k, n, k)
+        ws = []
+        for _ in range(24):
+            tq, ts = (t_.clone() for t_ in base._keep)
+            ws.append(q8.Q8(tq.data_ptr(), ts.data_ptr(), (tq, ts)))
+        x = torch.from_numpy(np.random.default_rng(n).standard_normal((m, k)).astype(np.float32)).cuda()
+        out = torch.empty((m, n), dtype=torch.float32, device="cuda")
+        q8.pproj(x, ws[0], out, m, n, k)
+        t = _timed(torch, stream, lambda i: q8.pproj(x, ws[i % 24], out, m, n, k), reps)
+        fl = 2.0 * m * n * k
+        res[name] = {"us": round(t * 1e6, 2), "tflops": round(fl / t / 1e12, 1)}
+        total += t
+        flops += fl
+    res["us_per_layer"] = round(total * 1e6, 2)
+    res["tflops"] = round(flops / total / 1e12, 1)
+    res["frac_fp16_peak"] = round(flops / total / 1e12 / PEAK_FP16_TFLOPS, 4)
+    return res
+
+
 def config_long_audio(torch, stream, q8, reps=5):
     """16 stacked 30 s windows: fc1 M=24000 K=1280 N=5120 and fc2 M=24000
     K=5120 N=1280 Q8 GEMMs."""
@@ -510,6 +543,8 @@ def main():
         cfg["batched_decode"] = config_batched_decode(torch, stream, q8)
         log("decoder token (M=1, GEMV family)")
         cfg["decode_token"] = config_decode_token(torch, stream, q8)
+        log("sequence prefill (M=320)")
+        cfg["prefill"] = config_prefill(torch, stream, q8)
         log("long audio (M=24000)")
         cfg["long_audio"] = config_long_audio(torch, stream, q8)
         result["configs"] = cfg

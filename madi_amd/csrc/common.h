@@ -25,6 +25,10 @@ int cu_count();
 int workspace(size_t partial_bytes, size_t counters, float **partials, uint32_t **cnt);
 // Releases the fp16 GEMM's rocBLAS handle (madi_cleanup).
 void f16gemm_cleanup();
+// The MFMA GEMM with f32 activations (rounded to f16) and an f32 result, for
+// the batched projection's many-row calls (gemm.hip); shapes checked by the caller.
+int q8_gemm_f32io(const float *in, const void *qs, const void *scales, float *out, uint32_t m,
+                  uint32_t n, uint32_t k);
 // Resolves the current device's address of the allocation-free GEMM's fixed
 // scratch array and clears its counters (madi_init).
 int gemm_scratch_init();

@@ -77,17 +77,24 @@ constexpr int kCStride = kPanelsPerTile * kPanelRows * 2 + 16;  // epilogue tile
 constexpr uint32_t kMaxSplits = 4;  // split-K workgroups per tile
 constexpr int kSplitTile = 2;       // m-tiles per tile where 128-row tiles would split K
 
-template <int MT>
+// F32: the activations arrive as f32 (rounded to f16 on their way from LDS to
+// the MFMA) and the result leaves as f32 -- the batched projection's operand
+// types (the engine's f32 rows, staged to f16 for the GEMM).
+template <int MT, bool F32 = false>
 struct Geometry {
-  static constexpr int kStage = MT * 32 * 128;  // one A stage (32*MT rows x 64 f16)
+  static constexpr int kRowBytes = F32 ? 256 : 128;  // one A row of a 64-wide chunk
+  static constexpr int kStage = MT * 32 * kRowBytes;  // one A stage (32*MT rows)
   static constexpr int kRing = NA * kStage;
-  static constexpr int kCTile = 32 * MT * kCStride;
+  static constexpr int kCPitch = F32 ? kPanelsPerTile * kPanelRows * 4 + 16 : kCStride;
+  static constexpr int kCTile = 32 * MT * kCPitch;
   static constexpr int kLds = kRing > kCTile ? kRing : kCTile;
   // vector-memory instructions per wave per chunk, spread over the four
   // k-steps so the texture pipe never sees a burst: step 0 the first half of
-  // the A DMA (MT row groups of 8 rows), step 1 its second half and weight unit
-  // (0,0), step 2 units (0,1) and (1,0), step 3 unit (1,1) and the two scales
-  static constexpr int LA = MT;
+  // the A DMA (LA DMAs of 1 KiB: 8 f16 rows or 4 f32 rows each), step 1 its
+  // second half and weight unit (0,0), step 2 units (0,1) and (1,0), step 3
+  // unit (1,1) and the two scales
+  static constexpr int LA = F32 ? 2 * MT : MT;
+  static constexpr int LA0 = LA >= 2 ? (LA + 1) / 2 : 0;  // DMAs issued in step 0
   static constexpr int LW = 6;
   static constexpr int kPerChunk = LA + LW;
   static constexpr int kBeforeStep3 = LA + 3;  // issued in steps 0..2
@@ -173,8 +180,10 @@ __device__ inline void wait_then_barrier() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-// XOR swizzle of the A tile's 16-byte chunks within row `row`
+// XOR swizzle of the A tile's 16-byte chunks within row `row`: 8 per f16 row,
+// 16 per f32 row
 __device__ inline uint32_t a_swz(uint32_t row) { return (row >> 1) & 7; }
+__device__ inline uint32_t a_swz32(uint32_t row) { return row & 15; }
 
 // One chunk's int8 weight units and scales of the wave's two panels
 struct RawW {
@@ -210,21 +219,29 @@ __device__ inline void drain(RawW &a, RawW &b, RawW &c, RawW &d) {
 }
 
 // Per-wave load plan, fixed for the whole K loop.
-template <int MT>
+template <int MT, bool F32>
 struct Plan {
   desc_t wq, ws, wa, zero;  // weights, scales, activations, empty
   uint32_t w_soff[2];       // byte offset of panel (2*wave + t) in the weights
   uint32_t s_voff[2];       // per-lane byte offset of this lane's scale, panel t
-  uint32_t a_voff[MT];      // per-lane activation offsets of the wave's row groups,
-                            // less the DMA's instruction offset (1024 * group)
-  uint32_t a_lds;           // the wave's first row group within an A stage
+  uint32_t a_voff[Geometry<MT, F32>::LA];  // per-lane activation offsets of the wave's
+                            // DMAs, less each DMA's instruction offset (1024 * DMA)
+  uint32_t a_lds;           // the wave's first A row within an A stage
   uint32_t nchunks;
 };
 
-// Row-group DMA I of the wave's A tile for one chunk.
-template <int MT, int I>
-__device__ inline void dma_group(desc_t wa, const Plan<MT> &p, uint32_t c, uint32_t m0) {
-  dma16<I * 1024, I == 0>(wa, p.a_voff[I], c * 128, m0);
+// DMA I of the wave's share of one chunk's A stage.
+template <int MT, bool F32, int I>
+__device__ inline void dma_group(desc_t wa, const Plan<MT, F32> &p, uint32_t c, uint32_t m0) {
+  dma16<I * 1024, I == 0>(wa, p.a_voff[I], c * Geometry<MT, F32>::kRowBytes, m0);
+}
+// DMAs I .. END-1
+template <int MT, bool F32, int I, int END>
+__device__ inline void dma_range(desc_t wa, const Plan<MT, F32> &p, uint32_t c, uint32_t m0) {
+  if constexpr (I < END) {
+    dma_group<MT, F32, I>(wa, p, c, m0);
+    dma_range<MT, F32, I + 1, END>(wa, p, c, m0);
+  }
 }
 
 // Which of a chunk's prefetches (the A stage DA chunks ahead, the weights WD
@@ -242,9 +259,9 @@ enum Prefetch { kSel = 0, kLive = 1, kLast0 = 2, kLast1 = 3, kLast2 = 4, kLast3 
 // after them are outstanding) and `a` before its last k-step (chunk c+1's A
 // stage, issued in steps 0-1 of chunk c+2-NA).  The last trip issues fewer
 // loads, so fewer remain outstanding behind each target.
-template <int MT, int PF>
+template <int MT, bool F32, int PF>
 struct Waits {
-  using G = Geometry<MT>;
+  using G = Geometry<MT, F32>;
   static constexpr int raw = PF == kLast1 ? G::kPerChunk
                            : PF >= kLast2 ? 0
                                           : G::kVmRaw;
@@ -254,9 +271,10 @@ struct Waits {
 
 // The vector-memory issues of k-step s for chunk c's A stage (into `slot`) and
 // chunk cw's weights (into `w`).
-template <int MT, int PF>
+template <int MT, bool F32, int PF>
 __device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, uint32_t cw,
-                                   const Plan<MT> &p, uint32_t lane) {
+                                   const Plan<MT, F32> &p, uint32_t lane) {
+  using G = Geometry<MT, F32>;
   static_assert(DA == 4 && WD == 4, "the last trip's issue plan assumes four-chunk prefetch");
   if constexpr (PF >= kLast0) return;
   desc_t wa = p.wa, wq = p.wq, ws = p.ws;
@@ -269,16 +287,9 @@ __device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, ui
   constexpr bool W = true;
   const uint32_t m0 = lds_addr(slot) + p.a_lds;
   if (s == 0) {
-    if constexpr (MT >= 2) dma_group<MT, 0>(wa, p, c, m0);
-    if constexpr (MT >= 3) dma_group<MT, 1>(wa, p, c, m0);
+    dma_range<MT, F32, 0, G::LA0>(wa, p, c, m0);
   } else if (s == 1) {
-    if constexpr (MT == 1) dma_group<MT, 0>(wa, p, c, m0);
-    if constexpr (MT == 2) dma_group<MT, 1>(wa, p, c, m0);
-    if constexpr (MT == 3) dma_group<MT, 2>(wa, p, c, m0);
-    if constexpr (MT == 4) {
-      dma_group<MT, 2>(wa, p, c, m0);
-      dma_group<MT, 3>(wa, p, c, m0);
-    }
+    dma_range<MT, F32, G::LA0, G::LA>(wa, p, c, m0);
     if constexpr (W) vload16(w.u[0][0], wq, lane * 16, p.w_soff[0] + cw * 2048);
   } else if (s == 2) {
     if constexpr (W) {
@@ -301,6 +312,39 @@ __device__ inline void load_a_frags(const uint8_t *As, int s, uint32_t h, uint32
   for (int i = 0; i < MT; ++i)
     bf[i] = *reinterpret_cast<const f16x8 *>(As + (i * 32 + r) * 128 + phys);
 }
+
+// f32 activations: a fragment's 8 values (k = 32h + 8s .. +8 of row r) are two
+// 16-byte pieces of the 256-byte row, rounded to f16 once they have landed.
+struct F32Frag {
+  f32x4 lo, hi;
+};
+template <int MT>
+__device__ inline void load_a_frags(const uint8_t *As, int s, uint32_t h, uint32_t r,
+                                    F32Frag (&bf)[MT]) {
+  const uint32_t sw = a_swz32(r);  // rows i*32 + r share r & 15
+  const uint32_t p0 = ((8 * h + 2 * s) ^ sw) * 16, p1 = ((8 * h + 2 * s + 1) ^ sw) * 16;
+#pragma unroll
+  for (int i = 0; i < MT; ++i) {
+    bf[i].lo = *reinterpret_cast<const f32x4 *>(As + (i * 32 + r) * 256 + p0);
+    bf[i].hi = *reinterpret_cast<const f32x4 *>(As + (i * 32 + r) * 256 + p1);
+  }
+}
+// round to nearest even, as the engine's f32 -> f16 staging (kCvt32)
+__device__ inline f16x8 to_f16(const F32Frag &f) {
+  return (f16x8){(f16)f.lo.x, (f16)f.lo.y, (f16)f.lo.z, (f16)f.lo.w,
+                 (f16)f.hi.x, (f16)f.hi.y, (f16)f.hi.z, (f16)f.hi.w};
+}
+
+// What a k-step keeps of its activation fragments between their LDS read and
+// the MFMAs of the next step: the f16 fragments, or the raw f32 values
+template <bool F32>
+struct AFrag {
+  using T = f16x8;
+};
+template <>
+struct AFrag<true> {
+  using T = F32Frag;
+};
 
 // The k-step-s fragment of panel t: half (s & 1) of unit s >> 1.  The four
 // pairs go through perm, subtract and multiply stage by stage (four
@@ -334,9 +378,10 @@ constexpr int kSchedDSRead = 0x100;
 // Instruction order of one k-step: its LDS reads first (their latency hides
 // under this step's MFMAs), then each MFMA followed by up to three VALU ops
 // (the dequantisation, 24 per step) and a vector-memory issue.
-template <int MT>
+template <int MT, bool F32 = false>
 __device__ inline void schedule_step() {
-  __builtin_amdgcn_sched_group_barrier(kSchedDSRead, MT, 0);
+  if constexpr (F32) __builtin_amdgcn_sched_group_barrier(kSchedVALU, 4 * MT, 0);  // f32 -> f16
+  __builtin_amdgcn_sched_group_barrier(kSchedDSRead, F32 ? 2 * MT : MT, 0);
 #pragma unroll
   for (int i = 0; i < 2 * MT; ++i) {
     __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
@@ -347,18 +392,20 @@ __device__ inline void schedule_step() {
 
 // One chunk c.  On entry w holds chunk c's fragments except w[0][3] and
 // w[1][3] (made at step 0 from `cur`, chunk c's weights), `af` holds chunk c's step-0
-// activation fragments, and `nxt` receives chunk c+1's weights (loaded WD-1
-// chunks ago; waited for here).  `ld` (the same
-// register set as `cur`, free after step 0) receives chunk c+WD's weights.
-template <int MT, int PF, bool ODD>
-__device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint32_t lane,
+// activation fragments (f32: their raw values, rounded at the step's start),
+// and `nxt` receives chunk c+1's weights (loaded WD-1 chunks ago; waited for
+// here).  `ld` (the same register set as `cur`, free after step 0) receives
+// chunk c+WD's weights.
+template <int MT, bool F32, int PF, bool ODD>
+__device__ inline void chunk(uint8_t *smem, const Plan<MT, F32> &p, uint32_t c, uint32_t lane,
                              uint32_t h, uint32_t r, f32x16 (&acc)[2][MT], f16x8 (&w)[2][4],
-                             f16x8 (&af)[MT], const RawW &cur, RawW &nxt, RawW &ld) {
-  using G = Geometry<MT>;
+                             typename AFrag<F32>::T (&af)[MT], const RawW &cur, RawW &nxt,
+                             RawW &ld) {
+  using G = Geometry<MT, F32>;
   const uint8_t *At = smem + (c % NA) * G::kStage;
   const uint8_t *An = smem + ((c + 1) % NA) * G::kStage;
   uint8_t *Af = smem + ((c + DA) % NA) * G::kStage;
-  wait_weights<Waits<MT, PF>::raw>(nxt);
+  wait_weights<Waits<MT, F32, PF>::raw>(nxt);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     // the previous step's fragment reads (issued a whole step ago) have
@@ -366,39 +413,48 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT> &p, uint32_t c, uint3
     // odd chunks: the A stages of chunks c+1 and c+2 become visible, and the
     // stages of chunks c-1 and c retire (refilled from chunk c+DA-2 on); an
     // even chunk reads chunk c+1's stage, published one chunk earlier
-    if (s == 3 && ODD) wait_then_barrier<Waits<MT, PF>::a>();
+    if (s == 3 && ODD) wait_then_barrier<Waits<MT, F32, PF>::a>();
     __builtin_amdgcn_s_waitcnt(kLgkm0);
-    f16x8 an[MT];
+    f16x8 a16[MT];
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+      if constexpr (F32)
+        a16[i] = to_f16(af[i]);
+      else
+        a16[i] = af[i];
+    }
+    typename AFrag<F32>::T an[MT];
     if (s < 3)
       load_a_frags<MT>(At, s + 1, h, r, an);
     else
       load_a_frags<MT>(An, 0, h, r, an);
 #pragma unroll
     for (int i = 0; i < MT; ++i)
-      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[0][s], af[i], acc[0][i], 0, 0, 0);
+      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[0][s], a16[i], acc[0][i], 0, 0, 0);
     // each panel's step s-1 fragment was consumed last step, at least 2*MT
     // MFMAs before its refill here (no read-after-write wait states): its
     // next value is chunk c's own step-3 fragment at step 0, else chunk c+1's
     w[0][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 0, (s + 3) & 3);
 #pragma unroll
     for (int i = 0; i < MT; ++i)
-      acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[1][s], af[i], acc[1][i], 0, 0, 0);
+      acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[1][s], a16[i], acc[1][i], 0, 0, 0);
     w[1][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 1, (s + 3) & 3);
-    issue_loads<MT, PF>(s, Af, c + DA, ld, c + WD, p, lane);
+    issue_loads<MT, F32, PF>(s, Af, c + DA, ld, c + WD, p, lane);
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[i] = an[i];
-    schedule_step<MT>();
+    schedule_step<MT, F32>();
     __builtin_amdgcn_sched_barrier(0);
   }
 }
 
-template <int MT, int EPI, bool PADDED>
+template <int MT, int EPI, bool PADDED, bool F32 = false>
 __global__ __launch_bounds__(256) void q8_gemm_kernel(
-    const f16 *__restrict__ A, const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
+    const void *__restrict__ A, const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
     uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m, uint32_t tiles_n, uint32_t group_m,
-    uint32_t cper, uint32_t crem, f16 *__restrict__ Cout, const float *__restrict__ bias,
+    uint32_t cper, uint32_t crem, void *__restrict__ Cout, const float *__restrict__ bias,
     float *__restrict__ ws, uint32_t *__restrict__ cnt) {
-  using G = Geometry<MT>;
+  using G = Geometry<MT, F32>;
+  static_assert(!F32 || EPI == MADI_EPI_NONE, "f32 output has no bias epilogue");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G::kLds];
   __shared__ uint32_t arrived;
 
@@ -434,10 +490,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
 
   // ---- load plan.  Panels past N and rows past M are clamped to the last
   // valid one: their bytes are read but their results are never stored.
-  Plan<MT> p;
+  Plan<MT, F32> p;
   p.wq = make_desc(qs, N * K);
   p.ws = make_desc(sc, N * K / 16);
-  p.wa = make_desc(A, M * K * 2);
+  p.wa = make_desc(A, M * K * (F32 ? 4 : 2));
   p.zero = make_desc(A, 0);
   p.nchunks = nchunks;
 #pragma unroll
@@ -448,17 +504,19 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     p.s_voff[t] = pp * K * 2 + cb * 128 + lane * 2;  // panel pp's chunk c scales at pp*K + 64c elements
   }
 #pragma unroll
-  for (int i = 0; i < MT; ++i) {
-    // wave w copies row groups MT*w .. MT*w+MT-1 (8 rows each) of the stage
-    const uint32_t row = (MT * wave + i) * 8 + (lane >> 3);
-    const uint32_t q = (lane & 7) ^ a_swz(row);
+  for (int i = 0; i < G::LA; ++i) {
+    // wave w copies DMAs LA*w .. LA*w+LA-1 of the stage, 1 KiB each: 8 rows
+    // of 64 f16 or 4 rows of 64 f32
+    constexpr uint32_t kRowsPerDma = F32 ? 4 : 8;
+    const uint32_t row = (G::LA * wave + i) * kRowsPerDma + (lane >> (F32 ? 4 : 3));
+    const uint32_t q = F32 ? (lane & 15) ^ a_swz32(row) : (lane & 7) ^ a_swz(row);
     uint32_t m = m0 + row;
     m = m < M ? m : M - 1;
-    // the DMA adds its instruction offset 1024*i to both addresses (row group
-    // i starts 8*i rows, at least 1024*i bytes, into A, so this cannot wrap)
-    p.a_voff[i] = m * K * 2 + cb * 128 + q * 16 - 1024 * i;
+    // the DMA adds its instruction offset 1024*i to both addresses (DMA i
+    // starts kRowsPerDma*i rows, at least 1024*i bytes, into A, so this cannot wrap)
+    p.a_voff[i] = m * K * (F32 ? 4 : 2) + cb * G::kRowBytes + q * 16 - 1024 * i;
   }
-  p.a_lds = MT * wave * 1024;
+  p.a_lds = G::LA * wave * 1024;
 
   f32x16 acc[2][MT];
 #pragma unroll
@@ -480,13 +538,14 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     RawW &rw = j == -4 ? r0 : j == -3 ? r1 : j == -2 ? r2 : r3;
 #pragma unroll
     for (int st = 0; st < 4; ++st)
-      issue_loads<MT, kSel>(st, slot, (uint32_t)(j + DA), rw, (uint32_t)(j + WD), p, lane);
+      issue_loads<MT, F32, kSel>(st, slot, (uint32_t)(j + DA), rw, (uint32_t)(j + WD), p, lane);
   }
   // chunk 0's weights and the A stages of chunks 0 and 1 (chunk 0 reads
   // chunk 1's stage without a barrier of its own), then chunk 0's fragments
   wait_then_barrier<G::kVmPrologue>();
   wait_weights<G::kVmPrologue>(r0);
-  f16x8 w[2][4], af[MT];
+  f16x8 w[2][4];
+  typename AFrag<F32>::T af[MT];
 #pragma unroll
   for (int s = 0; s < 3; ++s) w[0][s] = dequant_frag(r0, 0, s);
 #pragma unroll
@@ -501,10 +560,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   if constexpr (PADDED) {
     const uint32_t cpad = (nchunks + WD - 1) / WD * WD;
     for (uint32_t c = 0; c < cpad; c += 4) {
-      chunk<MT, kSel, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-      chunk<MT, kSel, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-      chunk<MT, kSel, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-      chunk<MT, kSel, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+      chunk<MT, F32, kSel, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+      chunk<MT, F32, kSel, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+      chunk<MT, F32, kSel, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+      chunk<MT, F32, kSel, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
     }
   } else {
     // at least two trips (the host checks): the loop is never skipped, so the
@@ -512,16 +571,16 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     // copies on a path around it
     uint32_t c = 0;
     do {
-      chunk<MT, kLive, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-      chunk<MT, kLive, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-      chunk<MT, kLive, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-      chunk<MT, kLive, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+      chunk<MT, F32, kLive, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+      chunk<MT, F32, kLive, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+      chunk<MT, F32, kLive, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+      chunk<MT, F32, kLive, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
       c += 4;
     } while (c + 2 * WD <= nchunks);
-    chunk<MT, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-    chunk<MT, kLast1, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-    chunk<MT, kLast2, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-    chunk<MT, kLast3, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+    chunk<MT, F32, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+    chunk<MT, F32, kLast1, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+    chunk<MT, F32, kLast2, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+    chunk<MT, F32, kLast3, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
   }
 
   drain(r0, r1, r2, r3);
@@ -643,10 +702,37 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   // workgroup; rows past M fall outside the tile's buffer resource and are
   // dropped, columns past N are skipped per lane.
   uint8_t *Ct = smem;
-  const uint32_t n = p0 * kPanelRows + r * 8;
   const uint32_t rows = M - m0 < 32 * MT ? M - m0 : 32 * MT;
-  const __amdgpu_buffer_rsrc_t cr =
-      __builtin_amdgcn_make_buffer_rsrc(Cout + (size_t)m0 * N, 0, (int)(rows * N * 2), 0x00020000);
+  if constexpr (F32) {
+    // f32 result: a 1 KiB row segment per store (lane l: columns 4l .. 4l+3)
+    const uint32_t n = p0 * kPanelRows + lane * 4;
+    const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<float *>(Cout) + (size_t)m0 * N, 0, (int)(rows * N * 4), 0x00020000);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const uint32_t nl = (2 * wave + t) * kPanelRows;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 o = {acc[t][i][g * 4 + 0], acc[t][i][g * 4 + 1], acc[t][i][g * 4 + 2],
+                           acc[t][i][g * 4 + 3]};
+          *reinterpret_cast<f32x4 *>(Ct + (i * 32 + r) * G::kCPitch + (nl + g * 8 + h * 4) * 4) = o;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t row = i * 32 + wave * 8 + j;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * G::kCPitch + lane * 16);
+        if (n < N) __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * N + n) * 4, 0, kSc1);
+      }
+    }
+    return;
+  }
+  const uint32_t n = p0 * kPanelRows + r * 8;
+  const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+      static_cast<f16 *>(Cout) + (size_t)m0 * N, 0, (int)(rows * N * 2), 0x00020000);
   f32x4 b4[2][4];
   if constexpr (EPI != MADI_EPI_NONE) {
 #pragma unroll
@@ -756,8 +842,8 @@ int resolve_scratch(uint8_t **out) {
 // Where a launch keeps its split-K partials and counters.
 enum Scratch { kWorkspace = 0, kStatic = 1 };
 
-template <int MT, int EPI>
-int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const float *bias,
+template <int MT, int EPI, bool F32 = false>
+int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const float *bias,
                 uint32_t M, uint32_t N, uint32_t K, Scratch where) {
   const uint32_t tiles_m = (M + 32 * MT - 1) / (32 * MT);
   const uint32_t tiles_n = (N + 255) / 256;
@@ -792,14 +878,14 @@ int launch_gemm(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const fl
     if (n % WD || n < 2 * WD) padded = true;
   }
   if (padded)
-    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, true>), dim3(T, splits), dim3(kWaves * 64), 0,
-                       stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
+    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, true, F32>), dim3(T, splits), dim3(kWaves * 64),
+                       0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
                        bias, ws, cnt);
   else
-    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false>), dim3(T, splits), dim3(kWaves * 64), 0,
-                       stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
+    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false, F32>), dim3(T, splits), dim3(kWaves * 64),
+                       0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
                        bias, ws, cnt);
-  return check_launch("madi_q8_gemm");
+  return check_launch(F32 ? "madi_q8_pproj" : "madi_q8_gemm");
 }
 
 template <int MT>
@@ -865,6 +951,20 @@ namespace madi {
 int gemm_scratch_init() {
   uint8_t *base = nullptr;
   return resolve_scratch(&base);
+}
+
+// out[M][N] (f32) = f16(in[M][K] (f32)) . deq(W)^T through the MFMA GEMM
+// (the batched projection for many rows): 32- or 64-row tiles by the same
+// rule as the f16 GEMM.  The caller has checked the shapes (N % 32 == 0,
+// K % 64 == 0, 16-byte aligned in and out, operands below 2 GiB).
+int q8_gemm_f32io(const float *in, const void *qs, const void *scales, float *out, uint32_t m,
+                  uint32_t n, uint32_t k) {
+  const uint8_t *Q = static_cast<const uint8_t *>(qs);
+  const f16 *S = static_cast<const f16 *>(scales);
+  const uint32_t cus = (uint32_t)cu_count();
+  if (m <= 32 || (tile_count(m, n, 1) <= cus && split_count(tile_count(m, n, 4), k / kChunkK) == 1))
+    return launch_gemm<1, MADI_EPI_NONE, true>(in, Q, S, out, nullptr, m, n, k, kWorkspace);
+  return launch_gemm<2, MADI_EPI_NONE, true>(in, Q, S, out, nullptr, m, n, k, kWorkspace);
 }
 }  // namespace madi
 

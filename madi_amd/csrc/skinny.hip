@@ -330,6 +330,12 @@ int launch_rows(const Proj &a) {
 
 }  // namespace
 
+// Rows from which the batched projection runs as the MFMA GEMM.
+#ifndef MADI_PPROJ_GEMM_ROWS
+#define MADI_PPROJ_GEMM_ROWS 160
+#endif
+constexpr uint32_t kGemmRows = MADI_PPROJ_GEMM_ROWS;
+
 extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const void *scales,
                              uint32_t m, uint32_t n, uint32_t k) {
   if (!out || !in || !qs || !scales) return fail(MADI_ERR_NULL, "madi_q8_pproj: null pointer");
@@ -347,6 +353,17 @@ extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const 
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_pproj: madi_init has not succeeded");
   if (int rc = deferred_before_read(in, (size_t)m * k * 4)) return rc;
   if (int rc = deferred_before_write(out, (size_t)m * n * 4)) return rc;
+  // Many rows (sequence prefill): the MFMA GEMM dequantises each weight once
+  // per 32 or 64 rows of a tile that spans 256 outputs, where this kernel
+  // dequantises it once per 32-row slice of a single panel.  Its tiles take
+  // ~11 us however few rows they hold (one K loop), so it pays from 160 rows
+  // on wide or long weights; a 1280 x 1280 weight has too few tiles (measured,
+  // cold weights, M = 320: 1280->5120 12.3 vs 27.2 us, 1280->3840 12.2 vs
+  // 20.3, 5120->1280 19.0 vs 34.1, 1280->1280 11.2 vs 8.7).
+  if (m >= kGemmRows && (n >= 2048 || k >= 4096) && n % kPanelRows == 0 && aligned(in, 16) &&
+      aligned(out, 16) &&
+      (uint64_t)m * k * 4 < (1ull << 31) && (uint64_t)n * 256 < (1ull << 31))
+    return q8_gemm_f32io(in, qs, scales, out, m, n, k);
   const Proj a{out, in, static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), m, n, k};
   // a batch of up to 8 or 16 rows loads only those activation rows
   if (m <= 8) return launch_rows<8>(a);

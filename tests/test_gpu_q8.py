@@ -544,6 +544,41 @@ def test_pproj_parity(q, m, n, k):
     assert staged_ok(c, x, qs, sc)
 
 
+# From 160 rows, for weights 2048 wide or 4096 long, the batched projection
+# runs as the MFMA GEMM with f32 activations and an f32 result
+# (q8_gemm_kernel<MT, NONE, PADDED, true>): 32-row tiles, 64-row tiles, an
+# M tail, a padded K loop (5 chunks over 4096 outputs) and the 5120-wide K
+# split over workgroups; 1280 x 1280 stays on the skinny kernel.
+@pytest.mark.parametrize("m,n,k", [
+    (160, 5120, 1280), (320, 3840, 1280), (320, 5120, 1280), (161, 4096, 320),
+    (320, 1280, 5120), (700, 2560, 1280), (256, 1280, 1280),
+])
+def test_pproj_many_rows_gemm(q, m, n, k):
+    say(f"pproj (GEMM) m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 7 + n + k)
+    x = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    qs, sc = synth.q8_weight(rng, n, k)
+    c = _pproj(q, x, qs, sc)
+    assert np.all(np.isfinite(c))
+    ref = O.q8_proj(x, qs, sc, threads=16)
+    assert normwise(c, ref) <= TOL, normwise(c, ref)
+    assert staged_ok(c, x, qs, sc)
+
+
+def test_pproj_many_rows_one_hot(q):
+    """One-hot rows through the GEMM route: f32 results equal the dequantised
+    weights bit for bit (one exact product, exact fp32 sums, f32 store)."""
+    n, k = 2048, 256
+    rng = np.random.default_rng(19)
+    qs, sc = synth.q8_weight(rng, n, k)
+    ks = np.arange(170) % k
+    x = np.zeros((len(ks), k), np.float32)
+    x[np.arange(len(ks)), ks] = 1.0
+    c = _pproj(q, x, qs, sc)
+    ref = O.dequant_q8_f16(qs, sc)[ks].astype(np.float32)
+    assert np.array_equal(c, ref)
+
+
 def test_pproj_one_hot_is_dequant(q):
     """x = one-hot rows: out[m][n] = fp16_rne(q s) of column k_m, bit-exact."""
     n, k = 96, 128
