@@ -777,6 +777,353 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   }
 }
 
+// ---------------------------------------------------------------- K split inside a workgroup
+// For N = 1280 at M = 1500 with a long K (fc2, 5120 -> 1280) the 128 x 256
+// tiles number only 60.  Here a workgroup owns a 128-row x 64-column tile
+// (two panels) and its four waves split K four ways: wave w runs the K loop
+// over chunks [w * cw, (w + 1) * cw) with the per-wave work of the 256-column
+// kernel (two panels x four m-tiles per k-step, 32 MFMAs per chunk), its
+// weights streaming into VGPRs as there and its own 128 A rows into a private
+// two-stage LDS ring (the waves share nothing, so the K loop has no barrier).
+// At the end the four partial tiles meet in LDS: wave w sums m-tile w in wave
+// order (the result does not depend on timing) and runs the epilogue for it.
+// 240 such tiles fill the GPU with no partial sums through memory.
+namespace ks {
+constexpr int kMT = 4;                    // m-tiles (of 32 rows) per tile
+constexpr int kStage = kMT * 32 * 128;    // one chunk of A for 128 rows: 16 KiB
+constexpr int kWaveRing = 2 * kStage;     // a wave's private ring
+constexpr int kLds = kWaves * kWaveRing;  // 128 KiB
+// Vector-memory issues per chunk: the weights of chunk c + 4 (units in steps
+// 0, 1, 1, 2 and the two scales in step 2) and, in step 3, the 16 DMAs that
+// copy chunk c + 2's A into the stage chunk c has just finished reading.
+constexpr int kW = 6, kD = kMT * 4, kPer = kW + kD;
+// Waits: `raw` at a chunk's start (chunk c + 1's weights, issued in chunk
+// c - 3: after them that chunk's DMAs and two whole chunks), `a` before step
+// 3 (chunk c + 1's A, the last issues of chunk c - 1: after them only chunk
+// c's weight loads).  Chunk 0 follows a prologue whose first two virtual
+// chunks issue no DMAs; the last trip issues no weights and DMAs only in its
+// first two chunks.
+enum Phase { kFirst0 = 0, kLive = 1, kLast0 = 2, kLast1 = 3, kLast2 = 4, kLast3 = 5 };
+template <int PH>
+struct Waits {
+  static constexpr int raw = PH == kFirst0 ? 2 * kPer
+                           : PH == kLast1  ? kD + kPer + kD
+                           : PH == kLast2  ? 3 * kD
+                           : PH == kLast3  ? 0
+                                           : kD + 2 * kPer;
+  static constexpr int a = PH >= kLast0 ? 0 : kW;
+  static_assert(raw < 64 && a < 64, "vmcnt range");
+};
+constexpr int kPrologueWait = kW + kD;  // chunk 0's weights and A stage
+
+struct Plan {
+  desc_t wq, ws, wa;
+  uint32_t w_soff[2];      // byte offset of panel t (chunk 0)
+  uint32_t s_voff[2];      // this lane's scale of panel t, chunk 0
+  uint32_t a_voff[kD];     // per-lane offsets of the 16 row groups, less their
+                           // instruction offsets (1024 * (g & 3))
+  uint32_t cb;             // the wave's first chunk
+};
+
+// The 16 DMAs of chunk c's A (8 rows each) into stage `slot`: four M0 values
+// of four row groups each (instruction offsets 0 .. 3072).
+__device__ inline void dma_chunk(const Plan &p, uint8_t *slot, uint32_t c) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const uint32_t m0 = lds_addr(slot) + q * 4096;
+    const uint32_t so = (p.cb + c) * 128;
+    dma16<0, true>(p.wa, p.a_voff[4 * q + 0], so, m0);
+    dma16<1024, false>(p.wa, p.a_voff[4 * q + 1], so, m0);
+    dma16<2048, false>(p.wa, p.a_voff[4 * q + 2], so, m0);
+    dma16<3072, false>(p.wa, p.a_voff[4 * q + 3], so, m0);
+  }
+}
+
+__device__ inline void load_w(int s, RawW &w, uint32_t cw, const Plan &p, uint32_t lane) {
+  const uint32_t c = p.cb + cw;
+  if (s == 0) {
+    vload16(w.u[0][0], p.wq, lane * 16, p.w_soff[0] + c * 2048);
+  } else if (s == 1) {
+    vload16<1024>(w.u[0][1], p.wq, lane * 16, p.w_soff[0] + c * 2048);
+    vload16(w.u[1][0], p.wq, lane * 16, p.w_soff[1] + c * 2048);
+  } else if (s == 2) {
+    vload16<1024>(w.u[1][1], p.wq, lane * 16, p.w_soff[1] + c * 2048);
+    vload2(w.s[0], p.ws, p.s_voff[0], c * 128);
+    vload2(w.s[1], p.ws, p.s_voff[1], c * 128);
+  }
+}
+
+template <int N>
+__device__ inline void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Instruction order of a k-step: LDS reads, then MFMAs with the dequantisation
+// between them, the step's weight loads, and in step 3 the A DMAs.
+template <int S>
+__device__ inline void schedule_step() {
+  __builtin_amdgcn_sched_group_barrier(kSchedDSRead, kMT, 0);
+#pragma unroll
+  for (int i = 0; i < 2 * kMT; ++i) {
+    __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedVALU, 24 / (2 * kMT) + 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedVMEM, S == 3 ? 2 : 1, 0);
+  }
+}
+
+// One chunk c of the wave's range (cf. chunk() of the 256-column kernel).  `ld`
+// receives chunk c + 4's weights and stage c & 1, read through step 2, receives
+// chunk c + 2's A in step 3.
+template <int PH>
+__device__ inline void chunk(uint8_t *ring, const Plan &p, uint32_t c, uint32_t lane, uint32_t h,
+                             uint32_t r, f32x16 (&acc)[2][kMT], f16x8 (&w)[2][4],
+                             f16x8 (&af)[kMT], const RawW &cur, RawW &nxt, RawW &ld) {
+  uint8_t *At = ring + (c & 1) * kStage;
+  const uint8_t *An = ring + ((c + 1) & 1) * kStage;
+  constexpr bool kLoadW = PH <= kLive;
+  constexpr bool kDma = PH <= kLast1;
+  wait_weights<Waits<PH>::raw>(nxt);
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    if (s == 3) wait_vm<Waits<PH>::a>();  // chunk c + 1's A has landed in An
+    __builtin_amdgcn_s_waitcnt(kLgkm0);
+    f16x8 an[kMT];
+    if (s < 3)
+      load_a_frags<kMT>(At, s + 1, h, r, an);
+    else
+      load_a_frags<kMT>(An, 0, h, r, an);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[0][s], af[i], acc[0][i], 0, 0, 0);
+    w[0][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 0, (s + 3) & 3);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+      acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[1][s], af[i], acc[1][i], 0, 0, 0);
+    w[1][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 1, (s + 3) & 3);
+    if constexpr (kLoadW) load_w(s, ld, c + WD, p, lane);
+    // step 3's reads of At (issued in step 2) were waited for above
+    if (s == 3 && kDma) dma_chunk(p, At, c + 2);
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) af[i] = an[i];
+    if (s == 3)
+      schedule_step<3>();
+    else
+      schedule_step<0>();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+}  // namespace ks
+
+template <int EPI>
+__global__ __launch_bounds__(256) void q8_gemm_ks_kernel(
+    const f16 *__restrict__ A, const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
+    uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m, uint32_t tiles_n, uint32_t group_m,
+    uint32_t cw, f16 *__restrict__ Cout, const float *__restrict__ bias) {
+  using ks::kMT;
+  using ks::kD;
+  using ks::kStage;
+  using ks::kWaveRing;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[ks::kLds];
+
+  // tile order as in q8_gemm_kernel: XCD-contiguous runs walked in groups of
+  // group_m M-tiles
+  const uint32_t T = tiles_m * tiles_n;
+  const uint32_t bid_x = blockIdx.x;
+  const uint32_t remap = 0u - (uint32_t)((T & 7) == 0);
+  const uint32_t bid = (((bid_x & 7) * (T >> 3) + (bid_x >> 3)) & remap) | (bid_x & ~remap);
+  const uint32_t per_group = group_m * tiles_n;
+  const uint32_t gi = bid / per_group, first_m = gi * group_m;
+  const uint32_t gm = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
+  const uint32_t tm = first_m + (bid % per_group) % gm;
+  const uint32_t tn = (bid % per_group) / gm;
+
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t h = lane >> 5, r = lane & 31;
+  const uint32_t m0 = tm * 32 * kMT, p0 = tn * 2;
+
+  ks::Plan p;
+  p.wq = make_desc(qs, N * K);
+  p.ws = make_desc(sc, N * K / 16);
+  p.wa = make_desc(A, M * K * 2);
+  p.cb = wave * cw;
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    // N % 64 == 0: both panels exist.  The chunk (the wave's base p.cb plus
+    // its own index) enters as the SGPR offset of every load.
+    const uint32_t pp = p0 + t;
+    p.w_soff[t] = pp * kPanelRows * K;
+    p.s_voff[t] = pp * K * 2 + lane * 2;
+  }
+#pragma unroll
+  for (int g = 0; g < kD; ++g) {
+    const uint32_t row = g * 8 + (lane >> 3);
+    const uint32_t q = (lane & 7) ^ a_swz(row);
+    uint32_t m = m0 + row;
+    m = m < M ? m : M - 1;
+    // row group g starts 8g rows, at least 1024 (g & 3) bytes, into A
+    p.a_voff[g] = m * K * 2 + q * 16 - 1024 * (g & 3);
+  }
+  uint8_t *ring = smem + wave * kWaveRing;
+
+  f32x16 acc[2][kMT];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) acc[t][i] = (f32x16){};
+
+  // prologue: virtual chunks -4 .. -1 issue the weights of chunks 0 .. 3, the
+  // last two also the A of chunks 0 and 1 (stages 0 and 1)
+  RawW r0, r1, r2, r3;
+#pragma unroll
+  for (int s = 0; s < 3; ++s) ks::load_w(s, r0, 0, p, lane);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) ks::load_w(s, r1, 1, p, lane);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) ks::load_w(s, r2, 2, p, lane);
+  ks::dma_chunk(p, ring, 0);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) ks::load_w(s, r3, 3, p, lane);
+  ks::dma_chunk(p, ring + kStage, 1);
+  ks::wait_vm<ks::kPrologueWait>();
+  wait_weights<ks::kPrologueWait>(r0);
+  f16x8 w[2][4], af[kMT];
+#pragma unroll
+  for (int s = 0; s < 3; ++s) w[0][s] = dequant_frag(r0, 0, s);
+#pragma unroll
+  for (int s = 0; s < 3; ++s) w[1][s] = dequant_frag(r0, 1, s);
+  load_a_frags<kMT>(ring, 0, h, r, af);
+
+  // first trip (chunk 0 follows the prologue), at least one live trip, last trip
+  ks::chunk<ks::kFirst0>(ring, p, 0, lane, h, r, acc, w, af, r0, r1, r0);
+  ks::chunk<ks::kLive>(ring, p, 1, lane, h, r, acc, w, af, r1, r2, r1);
+  ks::chunk<ks::kLive>(ring, p, 2, lane, h, r, acc, w, af, r2, r3, r2);
+  ks::chunk<ks::kLive>(ring, p, 3, lane, h, r, acc, w, af, r3, r0, r3);
+  uint32_t c = 4;
+  do {
+    ks::chunk<ks::kLive>(ring, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+    ks::chunk<ks::kLive>(ring, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+    ks::chunk<ks::kLive>(ring, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+    ks::chunk<ks::kLive>(ring, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+    c += 4;
+  } while (c + 2 * WD <= cw);
+  ks::chunk<ks::kLast0>(ring, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+  ks::chunk<ks::kLast1>(ring, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+  ks::chunk<ks::kLast2>(ring, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+  ks::chunk<ks::kLast3>(ring, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+  drain(r0, r1, r2, r3);
+
+  // ---- the four partial tiles meet: each wave hands the m-tiles it does not
+  // own to their owners through LDS (16-byte groups in register order, so each
+  // lane reads back what the same lane of the other wave wrote), then wave w
+  // adds the partials of m-tile w in wave order 0..3, its own from registers.
+  wait_then_barrier<0>();  // every wave is done with its ring
+  float *part = reinterpret_cast<float *>(smem);
+  auto slot = [&](uint32_t src, uint32_t i, int t, int g) {
+    return part + ((((src * kMT + i) * 2 + t) * 4 + g) * 64 + lane) * 4;
+  };
+#pragma unroll
+  for (int i = 0; i < kMT; ++i) {
+    if ((uint32_t)i == wave) continue;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4 *>(slot(wave, i, t, g)) =
+            (f32x4){acc[t][i][4 * g], acc[t][i][4 * g + 1], acc[t][i][4 * g + 2], acc[t][i][4 * g + 3]};
+  }
+  __syncthreads();
+  f32x16 fin[2];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    // the wave's own m-tile is index `wave`: select it from registers
+    f32x16 own = acc[t][0];
+#pragma unroll
+    for (int i = 1; i < kMT; ++i)
+      if ((uint32_t)i == wave) own = acc[t][i];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (uint32_t src = 0; src < (uint32_t)kWaves; ++src) {
+        const f32x4 o = {own[4 * g], own[4 * g + 1], own[4 * g + 2], own[4 * g + 3]};
+        const f32x4 v = src == wave ? o : *reinterpret_cast<const f32x4 *>(slot(src, wave, t, g));
+        sum = src == 0 ? v : sum + v;
+      }
+      fin[t][4 * g] = sum.x;
+      fin[t][4 * g + 1] = sum.y;
+      fin[t][4 * g + 2] = sum.z;
+      fin[t][4 * g + 3] = sum.w;
+    }
+  }
+  __syncthreads();  // partials read: the LDS becomes the output staging
+
+  // ---- epilogue of m-tile `wave`: bias / GELU, one rounding to f16, the
+  // 32 x 64 block transposed through the wave's own LDS region, stored as
+  // 128-byte row segments (lane l: row l/8 + 8j, columns 8 (l % 8) ..)
+  constexpr uint32_t kPitch = 64 * 2 + 16;
+  uint8_t *Ct = smem + wave * 32 * kPitch;
+  const uint32_t rows = M - m0 < 32 * kMT ? M - m0 : 32 * kMT;
+  const __amdgpu_buffer_rsrc_t cr =
+      __builtin_amdgcn_make_buffer_rsrc(Cout + (size_t)m0 * N, 0, (int)(rows * N * 2), 0x00020000);
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      float v[4] = {fin[t][4 * g], fin[t][4 * g + 1], fin[t][4 * g + 2], fin[t][4 * g + 3]};
+      if constexpr (EPI != MADI_EPI_NONE) {
+        const f32x4 b = *reinterpret_cast<const f32x4 *>(bias + (p0 + t) * kPanelRows + g * 8 + h * 4);
+        v[0] += b.x;
+        v[1] += b.y;
+        v[2] += b.z;
+        v[3] += b.w;
+        if constexpr (EPI == MADI_EPI_BIAS_GELU) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = gelu_erf_fast(v[e]);
+        }
+      }
+      const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+      *reinterpret_cast<f16x4 *>(Ct + r * kPitch + (32 * t + g * 8 + h * 4) * 2) = o;
+    }
+  }
+  const uint32_t n = p0 * kPanelRows + (lane & 7) * 8;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t row = (lane >> 3) + 8 * j;
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * kPitch + (lane & 7) * 16);
+    __builtin_amdgcn_raw_buffer_store_b128(v, cr, ((wave * 32 + row) * N + n) * 2, 0, kSc1);
+  }
+}
+
+// The per-wave chunk count of the in-workgroup K split, 0 when the shape does
+// not suit it: N a multiple of 64, K a multiple of 1024 with at least 12
+// chunks per wave (a first, a middle and a last trip of four), and 128 x 64
+// tiles that fill at least three quarters of the CUs in one round.  Each
+// wave streams its own A rows, four times the A traffic from L2 of the
+// 256-column tiles, so it only pays where those would split K through
+// memory: fc2 at M = 1500 (240 tiles) 29.3-29.6 -> 26.5-27.5 us with cold
+// weights; two rounds (N = 2048, K = 4096: 320 tiles) were slower (42.9 vs
+// 36.4 us), 160 tiles even (24.6 vs 24.7).
+#ifndef MADI_GEMM_KSPLIT
+#define MADI_GEMM_KSPLIT 1
+#endif
+uint32_t ks_chunks(uint32_t M, uint32_t N, uint32_t K) {
+  if (!MADI_GEMM_KSPLIT || N % 64 || K % 1024 || K / 256 < 12) return 0;
+  const uint32_t tiles = (M + 127) / 128 * (N / 64), cus = (uint32_t)cu_count();
+  return tiles * 4 >= cus * 3 && tiles <= cus ? K / 256 : 0;
+}
+
+template <int EPI>
+int launch_ks(const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C, const float *bias,
+              uint32_t M, uint32_t N, uint32_t K, uint32_t cw) {
+  const uint32_t tiles_m = (M + 127) / 128, tiles_n = N / 64;
+  const uint32_t group_m = tiles_m < 6 ? tiles_m : 6;
+  hipLaunchKernelGGL((q8_gemm_ks_kernel<EPI>), dim3(tiles_m * tiles_n), dim3(kWaves * 64), 0,
+                     stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cw, C, bias);
+  return check_launch("madi_q8_gemm");
+}
+
 // Too few tiles to fill the GPU and a long K (fc2 at M = 1500 with 64-row
 // tiles: 120 tiles, 80 chunks): split K over up to four workgroups per tile,
 // >= 16 chunks each.  The partial sums travel through memory (about 1 us per
@@ -926,11 +1273,21 @@ int q8_gemm(const char *what, const void *a, const void *qs, const void *scales,
   f16 *C = static_cast<f16 *>(c);
   if (m <= 32) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k, where);
   if (m <= 64) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k, where);
-  // Where 128-row tiles would split K: 64-row tiles, which halve the split
-  // count and the partial sums through memory (fc2 at M = 1500: 2 splits of
-  // 40 chunks instead of 4 of 20, 35 -> 30.5 us).
-  if (split_count(tile_count(m, n, 4), k / kChunkK) > 1)
+  // Where 128-row tiles would split K: the in-workgroup K split on 128 x 64
+  // tiles where the shape suits it (fc2 at M = 1500), else 64-row tiles, which
+  // halve the split count and the partial sums through memory (2 splits of
+  // 40 chunks instead of 4 of 20).
+  if (split_count(tile_count(m, n, 4), k / kChunkK) > 1) {
+    if (const uint32_t cw = ks_chunks(m, n, k)) {
+      switch (epilogue) {
+      case MADI_EPI_NONE: return launch_ks<MADI_EPI_NONE>(A, Q, S, C, bias, m, n, k, cw);
+      case MADI_EPI_BIAS: return launch_ks<MADI_EPI_BIAS>(A, Q, S, C, bias, m, n, k, cw);
+      case MADI_EPI_BIAS_GELU: return launch_ks<MADI_EPI_BIAS_GELU>(A, Q, S, C, bias, m, n, k, cw);
+      default: return fail(MADI_ERR_ARG, "%s: unknown epilogue %d", what, epilogue);
+      }
+    }
     return dispatch_epi<kSplitTile>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  }
   // Otherwise the lowest tiles whose count still fits one workgroup per CU:
   // a lower tile does less MFMA work per byte loaded (a 32-row tile takes
   // ~0.9x the time of a 64-row one for half the work) but spreads over more

@@ -220,6 +220,34 @@ def test_gemm_split_k(q, m, n, k):
         assert tight_ok(c, a, qs, sc)
 
 
+@pytest.mark.parametrize("m,n,k,epi", [
+    (1500, 1280, 6144, O.EPI_BIAS),       # 24 chunks per wave: four middle trips
+    (1500, 1280, 4096, O.EPI_BIAS_GELU),  # 16 per wave (one middle trip), a 92-row last m-tile
+    (1400, 1280, 5120, O.EPI_NONE),       # 20 per wave, 220 tiles, a 120-row last m-tile
+    (1500, 1280, 5120, O.EPI_BIAS),       # fc2: 240 tiles
+])
+def test_gemm_ksplit_in_workgroup(q, m, n, k, epi):
+    """Long K over few 128 x 256 tiles with N a multiple of 64: 128 x 64
+    tiles whose four waves split K and meet in LDS (q8_gemm_ks_kernel).  Row
+    sample over every 32-row boundary; a second run must give the same bits
+    (the partials are added in wave order)."""
+    say(f"gemm k-split in workgroup m={m} n={n} k={k} epi={epi}")
+    a, qs, sc = synth.gemm_case(m + k, m, n, k)
+    bias = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    b = None if epi == O.EPI_NONE else bias
+    c = _gemm(q, a, qs, sc, bias=b, gelu=epi == O.EPI_BIAS_GELU)
+    c2 = _gemm(q, a, qs, sc, bias=b, gelu=epi == O.EPI_BIAS_GELU)
+    assert np.array_equal(c.view(np.uint16), c2.view(np.uint16))
+    rows = tile_rows(m)
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, bias=b, epilogue=epi, threads=16)
+    assert normwise(c[rows], ref) <= TOL, normwise(c[rows], ref)
+    if epi == O.EPI_NONE:
+        assert tight_ok(c[rows], a[rows], qs, sc)
+    else:
+        assert tight_epi_ok(c[rows], a[rows], qs, sc, bias, epi == O.EPI_BIAS_GELU)
+    assert np.all(np.isfinite(c))
+
+
 def test_gemm_gelu_tails(q):
     """bias + GELU where the pre-activation spans +-40: the far negative tail
     must come out as (signed) zero and the positive tail as v itself, where

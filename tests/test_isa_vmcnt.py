@@ -37,6 +37,16 @@ def test_every_gemm_instance_is_race_free(gemm_asm):
     assert not bad, bad
 
 
+def test_every_ksplit_instance_is_race_free(gemm_asm):
+    """The in-workgroup K split (q8_gemm_ks_kernel, one instance per
+    epilogue): prologue, peeled first trip, K loop, last trip, reduction."""
+    names = [n for n in gemm_asm if "q8_gemm_ks_kernel" in n]
+    assert len(names) == 3, names
+    bad = {n: hazards(gemm_asm[n])[:3] for n in names}
+    bad = {n: b for n, b in bad.items() if b}
+    assert not bad, bad
+
+
 def test_checker_catches_a_premature_read():
     """The checker itself: a read of a load's destination before its wait,
     and a register reused while a dead load is in flight, are both flagged;
