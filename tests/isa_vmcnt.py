@@ -95,15 +95,55 @@ def _simulate(seq):
     return bad
 
 
+_LABEL = re.compile(r'^(\.LBB\w+):')
+
+
+def _loops(body_lines):
+    """{header label: (first line, last line, depth)} of every loop, from the
+    compiler's block annotations: a loop is its header block, the blocks
+    marked as inside it, and everything up to its last branch back into it."""
+    labels = {}
+    for i, l in enumerate(body_lines):
+        m = _LABEL.match(l.strip())
+        if m:
+            labels[m.group(1)] = i
+    out = {}
+    for lab, i in labels.items():
+        text = body_lines[i] + (body_lines[i + 1] if i + 1 < len(body_lines) else '')
+        m = re.search(r'Loop Header: Depth=(\d+)', text)
+        if not m:
+            continue
+        tag = lab.lstrip('.').replace('LBB', 'BB')
+        members = [j for l2, j in labels.items()
+                   if j == i or f'Header={tag} ' in body_lines[j] + ' '
+                   or f'Parent Loop {tag} ' in body_lines[j] + ' ']
+        names = {l2 for l2, j in labels.items() if j in members}
+        start = min(members)
+        last = max(j for j, l in enumerate(body_lines)
+                   if ('s_cbranch' in l or 's_branch' in l) and l.split()[-1] in names
+                   and j >= start)
+        out[lab] = (start, last, int(m.group(1)), i)
+    return out
+
+
 def hazards(body_lines, iters: int = 3):
     """Hazards on the path prologue -> loop body x iters -> rest, for the
-    kernel's first loop (the K loop)."""
-    hdr = next((i for i, l in enumerate(body_lines) if 'Loop Header' in l), None)
-    if hdr is None:
+    kernel's first loop (the K loop).  When the first loop holds a nested loop
+    (a tile loop around the K loop), the path is prologue -> (outer body with
+    the inner body x iters) x 2 -> rest, the outer body entered at its header
+    (blocks the compiler placed before the header run after it)."""
+    loops = _loops(body_lines)
+    if not loops:
         return _simulate(_parse(body_lines))
-    label = body_lines[hdr].split(':')[0].strip()
-    end = next(i for i, l in enumerate(body_lines)
-               if i > hdr and 's_cbranch' in l and l.split()[-1] == label)
-    pro, loop, post = (_parse(body_lines[:hdr]), _parse(body_lines[hdr + 1:end]),
-                       _parse(body_lines[end + 1:]))
-    return _simulate(pro + loop * iters + post)
+    outer = min(loops.values(), key=lambda v: v[0])
+    start, last, depth, hdr = outer
+    pre, post = _parse(body_lines[:start]), _parse(body_lines[last + 1:])
+    inner = [v for v in loops.values() if v[2] == depth + 1 and start <= v[0] <= last]
+    if not inner:
+        body = _parse(body_lines[hdr:last + 1]) + _parse(body_lines[start:hdr])
+        return _simulate(pre + body * iters + post)
+    istart, ilast, _, _ = min(inner, key=lambda v: v[0])
+    main = (_parse(body_lines[hdr:istart]) + _parse(body_lines[istart:ilast + 1]) * iters
+            + _parse(body_lines[ilast + 1:last + 1]))
+    body = main + _parse(body_lines[start:hdr])
+    return _simulate(pre + body * 2 + post)

@@ -355,6 +355,38 @@ def test_gemm_long_audio_full_m(q, name, n, k):
     assert np.all(np.isfinite(c))
 
 
+@pytest.mark.parametrize("m,n,k,epi", [
+    (24000, 5120, 1280, O.EPI_NONE),       # long-audio fc1: 3760 tiles, 14.7 per workgroup
+    (24000, 5120, 1280, O.EPI_BIAS_GELU),  # ... with bias + GELU
+    (7001, 4096, 768, O.EPI_BIAS_GELU),    # 12-chunk K (first trip, one middle, last), M tail of 89 rows
+    (13300, 1280, 2048, O.EPI_BIAS),       # 520 tiles: two rounds and 8 tiles, 32-chunk K, M tail of 116
+])
+def test_gemm_persistent(q, m, n, k, epi):
+    """At least two rounds of 128 x 256 tiles: the persistent tile loop
+    (q8_gemm_persist_kernel) issues each next tile's loads before the
+    finished tile's epilogue.  Row sample over tile boundaries and the tail;
+    a second run gives the same bits."""
+    say(f"gemm persistent m={m} n={n} k={k} epi={epi}")
+    rng = np.random.default_rng(m + n)
+    a = synth.activations(rng, m, k)
+    qs, sc = synth.q8_weight(rng, n, k)
+    bias = rng.standard_normal(n).astype(np.float32)
+    b = None if epi == O.EPI_NONE else bias
+    c = _gemm(q, a, qs, sc, bias=b, gelu=epi == O.EPI_BIAS_GELU)
+    c2 = _gemm(q, a, qs, sc, bias=b, gelu=epi == O.EPI_BIAS_GELU)
+    assert np.array_equal(c.view(np.uint16), c2.view(np.uint16))
+    rows = np.unique(np.r_[0, 31, 32, 127, 128, 255, 256, (m // 128) * 128 - 1, (m // 128) * 128,
+                           m // 2, m - 33, m - 1, rng.integers(0, m, 24)])
+    rows = rows[(rows >= 0) & (rows < m)]
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, bias=b, epilogue=epi, threads=16)
+    assert normwise(c[rows], ref) <= TOL, normwise(c[rows], ref)
+    if epi == O.EPI_NONE:
+        assert tight_ok(c[rows], a[rows], qs, sc)
+    else:
+        assert tight_epi_ok(c[rows], a[rows], qs, sc, bias, epi == O.EPI_BIAS_GELU)
+    assert np.all(np.isfinite(c))
+
+
 def test_gemm_large_m(q):
     """Several tiles per CU (M = 6657: 53 x 20 tiles of 128 x 256, a 1-row M
     tail); row sample over tile boundaries."""

@@ -47,6 +47,17 @@ def test_every_ksplit_instance_is_race_free(gemm_asm):
     assert not bad, bad
 
 
+def test_every_persistent_instance_is_race_free(gemm_asm):
+    """The persistent tile loop (q8_gemm_persist_kernel, one instance per
+    epilogue): two trips of the tile loop, each with the K loop three times,
+    the next tile's prologue issued before the finished tile's epilogue."""
+    names = [n for n in gemm_asm if "q8_gemm_persist_kernel" in n]
+    assert len(names) == 3, names
+    bad = {n: hazards(gemm_asm[n])[:3] for n in names}
+    bad = {n: b for n, b in bad.items() if b}
+    assert not bad, bad
+
+
 def test_checker_catches_a_premature_read():
     """The checker itself: a read of a load's destination before its wait,
     and a register reused while a dead load is in flight, are both flagged;
