@@ -205,8 +205,10 @@ int madi_q8_pproj(float *out, const float *in, const void *qs, const void *scale
  * "dequant_q8_f16", "m4_gemm_nn", "m4_gemm_bias", "m4_gemm_bias_gelu",
  * "gemv_q8", "gemv_q8_bias", "gemv_q8_bias_gelu", "gemv_q8_bias_res",
  * "gemv_q8_qkv", "logit_gemv_q8", "gpu_emb_lookup_q8",
- * "emb_lookup_indirect_q8", "emb_pe_rows_q8", "mul_mm_q8".  Another name
- * fails with MADI_ERR_ARG (FunctionNotFound).  Needs no device. */
+ * "emb_lookup_indirect_q8", "emb_pe_rows_q8", "mul_mm_q8", and the
+ * encoder attention kernels "m4_flash_enc" and "flash_attention_enc_f16"
+ * (both run madi_flash_enc_f16).  Another name fails with MADI_ERR_ARG
+ * (FunctionNotFound).  Needs no device. */
 int madi_get_function(const char *name, int *out_id);
 /* kM4 / kM4Bias (engine/metal/encoder.zig:125-136) with the handle the engine
  * resolved: m4_gemm_nn (bias ignored), m4_gemm_bias or m4_gemm_bias_gelu, on
@@ -276,6 +278,20 @@ int madi_q8_emb_lookup_indirect(float *out, const void *qs, const void *scales,
  * token >= vocab leaves its row untouched.  out and pe 16-byte aligned. */
 int madi_q8_emb_pe_rows(float *out, const void *qs, const void *scales, const uint32_t *tokens,
                         const float *pe, uint32_t dim, uint32_t pos0, uint32_t m, uint32_t vocab);
+
+/* ---- encoder self-attention over the projections ------------------------------ */
+/* m4_flash_enc (engine/metal/kernels/m4_gemm.metal:268-407; buffers 0-5 in this
+ * order), which kFlash (engine/metal/encoder.zig:138-152) dispatches once per
+ * window on the Q, K, V projections: bidirectional attention with head dim 64,
+ * out = softmax(q k^T / 8) v per head, in the reference's arithmetic (f32
+ * scores, an online softmax over 64-key blocks, f16 P, f32 sums, out =
+ * f16(O / (sum + 1e-6))).  q, k, v, out: f16 [seq_len][nh*64], head h in
+ * columns 64h..64h+63.  Unlike the reference kernel, q/k/v need no padding
+ * rows past seq_len.  All four 16-byte aligned; out must not overlap k or v
+ * (out == q is allowed: each query row is read before its output is
+ * written); seq_len = 0 does nothing; seq_len * nh * 128 <= 2 GiB. */
+int madi_flash_enc_f16(void *out, const void *q, const void *k, const void *v, uint32_t seq_len,
+                       uint32_t nh);
 
 #ifdef __cplusplus
 }

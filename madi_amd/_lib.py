@@ -66,6 +66,7 @@ SIGNATURES = {
     "madi_q8_emb_lookup": (_I, [_P, _P, _P, _P, _U32, _U32]),
     "madi_q8_emb_lookup_indirect": (_I, [_P, _P, _P, _P, _P, _U32, _U32]),
     "madi_q8_emb_pe_rows": (_I, [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32]),
+    "madi_flash_enc_f16": (_I, [_P, _P, _P, _P, _U32, _U32]),
 }
 
 

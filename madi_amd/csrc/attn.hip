@@ -1,0 +1,331 @@
+// attn.hip -- encoder self-attention over the Q/K/V projections, the consumer
+// of the encoder's projection GEMMs: replaces m4_flash_enc
+// (engine/metal/kernels/m4_gemm.metal:268-407), which kFlash dispatches once
+// per 30 s window (engine/metal/encoder.zig:138-152, called at :281-283).
+//
+// Arithmetic, as the reference's: S = Q K^T in f32 from f16 operands, scaled
+// by 1/8; an online softmax over 64-key blocks against a running row max;
+// P = f16(e); O += P V in f32; out = f16(O / (sum + 1e-6)).  Two changes that
+// move only roundings: e is the hardware exp2 of s * log2(e)/8 - m', and the
+// reference max m' is raised only when a block's max passes it by more than 8
+// (log2 units), so e <= 256 (well inside f16, each P still rounded relative to
+// its own magnitude) and O and the sum are rescaled in a few blocks instead of
+// in every block.  The sum adds the unrounded e, as the reference's does.
+//
+// Layout: q, k, v, out f16 [seq][nh*64], head hd in columns 64hd..64hd+63 (the
+// projection GEMMs' output, unpadded: rows past seq are never read -- row
+// indices clamp to the last row, and the keys past seq get weight 0).
+//
+// Workgroup: 128 query rows of one head.  A key group of 4 waves walks the
+// keys; wave w owns query rows 32w..32w+31 (the MFMA's 32 columns).  KS = 2
+// splits the key range between two such groups (two waves per SIMD, whose
+// matrix and vector work interleave); their partial (m', sum, O) meet in LDS
+// at the end.  Per 64-key block a wave computes
+//   S^T = K Q^T: two v_mfma_f32_32x32x16_f16 tiles with the keys as rows, so
+//     lane (h, r) holds query r's scores of keys 32t + 8j + 4h + i
+//     (s[t][4j + i]): row max and sum are in-lane plus one exchange between
+//     the lane halves;
+//   O^T += V^T P^T: two tiles with d as rows; P^T comes straight from the S^T
+//     registers as the B operand (k slot 8h + 4jj + i of MFMA (t, a) is key
+//     32t + 16a + 8jj + 4h + i), and V^T from the untransposed V tile through
+//     the LDS transpose read (ds_read_b64_tr_b16: 16 lanes pass 4 rows x 16
+//     columns of f16, lane c receives column c), which gives each lane one d
+//     and four consecutive keys.
+// The K and V tiles of a block (64 rows x 128 bytes each) arrive by LDS DMA in
+// a 3-stage ring per key group, two blocks ahead, with one barrier per block;
+// the 16-byte pieces of each row are XOR-swizzled so that the K fragment reads
+// (32 rows, one piece each) and the transpose reads (8 rows x 64 bytes) spread
+// over all banks.
+#include "common.h"
+#include "vmem.h"
+
+using namespace madi;
+
+namespace {
+
+constexpr int kQRows = 128;                        // query rows per workgroup
+constexpr int kTileBytes = 64 * 64 * 2;            // one K or V tile: 64 keys x 64 d
+constexpr int kStageBytes = 2 * kTileBytes;        // K tile, then V tile
+constexpr int kRingBytes = 3 * kStageBytes;        // per key group
+constexpr float kScaleLog2 = 0.125f * 1.4426950408889634f;  // 1/8 * log2(e)
+constexpr float kLazy = 8.0f;  // raise the reference max when exceeded by more than this
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+
+// piece swizzles: K rows (fragment reads of 32 rows at one piece), V rows
+// (transpose reads of 4 consecutive rows x 4 pieces per half-wave)
+__device__ inline uint32_t swz_k(uint32_t row) { return (row >> 1) & 7; }
+__device__ inline uint32_t swz_v(uint32_t row) { return ((row >> 1) & 1) << 2; }
+
+__device__ inline f16x8 lds_read16(uint32_t addr) {
+  return __builtin_bit_cast(f16x8, *(const lds_u32x4 *)(uintptr_t)addr);
+}
+__device__ inline f16x4 lds_read_tr(uint32_t addr) {
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4 *)(uintptr_t)addr));
+}
+
+// Wait for the Q fragments and every DMA issued so far, then meet the other
+// waves; the fragments are operands, so no use of them is scheduled before
+// the wait.
+__device__ inline void wait_q_then_barrier(u32x4 (&qf)[4]) {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier"
+               : "+v"(qf[0]), "+v"(qf[1]), "+v"(qf[2]), "+v"(qf[3])
+               :
+               : "memory");
+}
+
+// Grid: one workgroup per (head, 128-row query tile), 256 * KS threads.
+template <int KS>
+__global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
+    f16 *__restrict__ out, const f16 *__restrict__ q, const f16 *__restrict__ k,
+    const f16 *__restrict__ v, uint32_t seq, uint32_t nh, uint32_t qtiles) {
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[KS * kRingBytes];
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = sgpr(threadIdx.x >> 6);
+  const uint32_t grp = wave >> 2, wq = wave & 3;
+  const uint32_t h = lane >> 5, r = lane & 31;
+
+  // Workgroups x and x + 8 run on the same XCD (round-robin dispatch): each
+  // XCD takes a contiguous run of (head, query tile) items, heads outermost,
+  // so a head's K and V rows are fetched into one or two L2s.
+  const uint32_t items = nh * qtiles, b = blockIdx.x, x = b & 7;
+  const uint32_t per = items >> 3, extra = items & 7;
+  const uint32_t item = x * per + (x < extra ? x : extra) + (b >> 3);
+  const uint32_t head = item / qtiles, qt = item - head * qtiles;
+
+  const uint32_t rowb = nh * 128;  // bytes per sequence row
+  const uint32_t bytes = seq * rowb;
+  const desc_t dq = make_desc(q, bytes), dk = make_desc(k, bytes), dv = make_desc(v, bytes);
+
+  // Q^T fragments (B operand of S^T): query row q0 + r, d = 16s + 8h .. +7
+  const uint32_t q0 = qt * kQRows + wq * 32;
+  const uint32_t qrow = min(q0 + r, seq - 1);
+  u32x4 qf[4];
+  {
+    const uint32_t qv = qrow * rowb + head * 128 + h * 16;
+    vload16<0>(qf[0], dq, qv, 0);
+    vload16<32>(qf[1], dq, qv, 0);
+    vload16<64>(qf[2], dq, qv, 0);
+    vload16<96>(qf[3], dq, qv, 0);
+  }
+
+  // key blocks of this wave's group
+  const uint32_t nb = (seq + 63) >> 6;
+  uint32_t kb0 = 0, nblk = nb, iters = nb;
+  if constexpr (KS == 2) {
+    const uint32_t nb0 = (nb + 1) >> 1;
+    kb0 = grp ? nb0 : 0;
+    nblk = grp ? nb - nb0 : nb0;
+    iters = nb0;
+  }
+  const uint32_t ring = lds_addr(smem) + grp * kRingBytes;
+
+  // DMA plan: wave wq copies rows 16wq .. 16wq+15 of the K and V tiles, 8 rows
+  // per DMA; lane -> row 16wq + 8i + lane/8, LDS piece lane%8, which holds the
+  // row's logical piece (lane%8) ^ swizzle(row)
+  uint32_t drow[2], kpiece[2], vpiece[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    drow[i] = 16 * wq + 8 * i + (lane >> 3);
+    kpiece[i] = head * 128 + 16 * ((lane & 7) ^ swz_k(drow[i]));
+    vpiece[i] = head * 128 + 16 * ((lane & 7) ^ swz_v(drow[i]));
+  }
+  auto issue = [&](uint32_t blk, uint32_t stage) {
+    const uint32_t kv0 = (kb0 + blk) * 64;
+    const uint32_t kt = ring + stage * kStageBytes + 16 * wq * 128;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint32_t row = min(kv0 + drow[i], seq - 1) * rowb;
+      dma16<0, true>(dk, row + kpiece[i], 0, kt + i * 1024);
+      dma16<0, true>(dv, row + vpiece[i], 0, kt + kTileBytes + i * 1024);
+    }
+  };
+  if (nblk > 0) issue(0, 0);
+  if (nblk > 1) issue(1, 1);
+  // one unconditional wait for Q and both first blocks: the fragments pass
+  // through a single asm statement, so the compiler has no merged copy of
+  // them to make before the wait
+  wait_q_then_barrier(qf);
+  f16x8 qh[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) qh[s] = __builtin_bit_cast(f16x8, qf[s]);
+
+  // lane constants of the fragment reads: K row r at piece 2s + h; V^T via
+  // transpose reads: lane (g = lane/16, c = lane%16) passes row 4h + c/4 of a
+  // 4-row group, columns 32dd + 16(g%2) + 4(c%4) .. +3
+  const uint32_t k_row = r * 128, k_swz = swz_k(r);
+  uint32_t v_off[2];
+  {
+    const uint32_t c = lane & 15, rr = c >> 2, cc = c & 3;
+    const uint32_t vrow = 4 * h + rr;
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd) {
+      const uint32_t piece = 4 * dd + 2 * ((lane >> 4) & 1) + (cc >> 1);
+      v_off[dd] = vrow * 128 + 16 * (piece ^ swz_v(vrow)) + 8 * (cc & 1);
+    }
+  }
+
+  f32x16 o[2] = {};
+  float mref = -__builtin_inff(), l = 0.0f;
+  uint32_t stage = 0;
+  for (uint32_t j = 0; j < iters; ++j) {
+    if (j + 2 < nblk) issue(j + 2, stage == 0 ? 2 : stage - 1);
+    if (j < nblk) {
+      const uint32_t kt = ring + stage * kStageBytes, vt = kt + kTileBytes;
+      const uint32_t kv0 = (kb0 + j) * 64;
+      f32x16 s[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        s[t] = (f32x16){};
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+          const f16x8 kf = lds_read16(kt + t * 32 * 128 + k_row + 16 * ((2 * st + h) ^ k_swz));
+          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[st], s[t], 0, 0, 0);
+        }
+      }
+      if (kv0 + 64 > seq) {  // the last block: keys past seq take no weight
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int e = 0; e < 16; ++e)
+            if (kv0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3) >= seq) s[t][e] = -__builtin_inff();
+      }
+      float mx = s[0][0];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) mx = __builtin_fmaxf(mx, s[t][e]);
+      mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = mx * kScaleLog2;
+      const bool up = mnew > mref + kLazy;
+      if (__builtin_amdgcn_ballot_w64(up)) {
+        const float nref = up ? mnew : mref;
+        const float alpha = __builtin_amdgcn_exp2f(mref - nref);  // 0 on the first block
+        l *= alpha;
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[dd][e] *= alpha;
+        mref = nref;
+      }
+      const float nm = -mref;
+      f16x8 p[2][2];
+      float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int a = 0; a < 2; ++a)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * a + e], kScaleLog2, nm));
+            ls[e & 3] += ex;
+            p[t][a][e] = (f16)ex;
+          }
+      l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int a = 0; a < 2; ++a) {
+            const uint32_t base = vt + (32 * t + 16 * a) * 128 + v_off[dd];
+            const f16x4 lo = lds_read_tr(base), hi = lds_read_tr(base + 8 * 128);
+            const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            o[dd] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, p[t][a], o[dd], 0, 0, 0);
+          }
+    }
+    // block j + 1 has landed (block j + 2's DMAs may be in flight) and every
+    // wave is done with block j's stage
+    if (j + 2 < nblk)
+      wait_then_barrier<4>();
+    else
+      wait_then_barrier<0>();
+    stage = stage == 2 ? 0 : stage + 1;
+  }
+  // each lane summed the weights of its own 32 keys per block; the two lane
+  // halves share the reference max, so their sums add
+  l += __shfl_xor(l, 32);
+
+  if constexpr (KS == 2) {
+    // the second key group hands (m', sum, O) to the first through LDS (the
+    // ring is free: every wave passed the loop's last barrier)
+    float *xch = reinterpret_cast<float *>(smem) + wq * 34 * 64;
+    if (grp == 1) {
+      xch[lane] = mref;
+      xch[64 + lane] = l;
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) xch[(2 + 16 * dd + e) * 64 + lane] = o[dd][e];
+    }
+    __syncthreads();
+    if (grp == 1) return;
+    const float mb = xch[lane], lb = xch[64 + lane];
+    const float m = __builtin_fmaxf(mref, mb);
+    const float fa = __builtin_amdgcn_exp2f(mref - m), fb = __builtin_amdgcn_exp2f(mb - m);
+    l = l * fa + lb * fb;
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[dd][e] = o[dd][e] * fa + xch[(2 + 16 * dd + e) * 64 + lane] * fb;
+  }
+
+  // out row q0 + r, d = 32dd + 8g + 4h + i from o[dd][4g + i]
+  const uint32_t orow = q0 + r;
+  if (orow < seq) {
+    const float inv = 1.0f / (l + 1e-6f);
+    f16 *dst = out + (size_t)orow * nh * 64 + head * 64 + 4 * h;
+#pragma unroll
+    for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f16x4 val = {(f16)(o[dd][4 * g] * inv), (f16)(o[dd][4 * g + 1] * inv),
+                           (f16)(o[dd][4 * g + 2] * inv), (f16)(o[dd][4 * g + 3] * inv)};
+        *reinterpret_cast<f16x4 *>(dst + 32 * dd + 8 * g) = val;
+      }
+  }
+}
+
+bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
+  const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+  return x < y + bn && y < x + an;
+}
+
+// Key groups per workgroup: two (two waves per SIMD) while the workgroups do
+// not fill the compute units twice over.
+int key_groups(uint32_t items) {
+  if (const char *e = getenv("MADI_FLASH_KSPLIT")) return atoi(e) == 1 ? 1 : 2;
+  return items < 2u * (uint32_t)cu_count() ? 2 : 1;
+}
+
+}  // namespace
+
+extern "C" int madi_flash_enc_f16(void *out, const void *q, const void *k, const void *v,
+                                  uint32_t seq_len, uint32_t nh) {
+  if (!out || !q || !k || !v) return fail(MADI_ERR_NULL, "madi_flash_enc_f16: null pointer");
+  if (nh == 0) return fail(MADI_ERR_SHAPE, "madi_flash_enc_f16: nh must be at least 1");
+  const size_t bytes = (size_t)seq_len * nh * 128;
+  if (bytes > ((size_t)1 << 31))
+    return fail(MADI_ERR_SHAPE, "madi_flash_enc_f16: seq_len * nh * 64 f16 = %zu bytes exceeds 2 GiB", bytes);
+  if (!aligned(out, 16) || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16))
+    return fail(MADI_ERR_ALIGN, "madi_flash_enc_f16: out, q, k and v must be 16-byte aligned");
+  if (overlaps(out, bytes, k, bytes) || overlaps(out, bytes, v, bytes) ||
+      (out != q && overlaps(out, bytes, q, bytes)))
+    return fail(MADI_ERR_ARG, "madi_flash_enc_f16: out overlaps k or v (or q other than exactly)");
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_flash_enc_f16: madi_init has not succeeded");
+  if (seq_len == 0) return MADI_OK;  // no query rows (the reference's grid is empty)
+  for (const void *in : {q, k, v})
+    if (int rc = deferred_before_read(in, bytes)) return rc;
+  if (int rc = deferred_before_write(out, bytes)) return rc;
+  const uint32_t qtiles = (seq_len + kQRows - 1) / kQRows;
+  const uint32_t items = nh * qtiles;
+  if (key_groups(items) == 2)
+    flash_enc_kernel<2><<<items, 512, 0, stream()>>>((f16 *)out, (const f16 *)q, (const f16 *)k,
+                                                     (const f16 *)v, seq_len, nh, qtiles);
+  else
+    flash_enc_kernel<1><<<items, 256, 0, stream()>>>((f16 *)out, (const f16 *)q, (const f16 *)k,
+                                                     (const f16 *)v, seq_len, nh, qtiles);
+  return check_launch("madi_flash_enc_f16");
+}

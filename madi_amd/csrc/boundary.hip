@@ -50,14 +50,15 @@ enum Fn {
   kFnEmbIndirect,
   kFnEmbPeRows,
   kFnMulMmQ8,
+  kFnFlashEnc,
 };
 
 struct FnName {
   const char *name;
   Fn id;
 };
-// kernels/q8_gemm.metal:12, 29; m4_gemm.metal:19, 60, 88; graph_helpers.metal:320,
-// 354, 370, 390, 424, 475, 498, 527; decoder_ops.metal:614
+// kernels/q8_gemm.metal:12, 29; m4_gemm.metal:19, 60, 88, 268; graph_helpers.metal:320,
+// 354, 370, 390, 424, 475, 498, 527; decoder_ops.metal:614; encoder_ops.metal:398
 constexpr FnName kFunctions[] = {
     {"dequant_q8_f16", kFnDeq},          {"m4_gemm_nn", kFnM4},
     {"m4_gemm_bias", kFnM4Bias},         {"m4_gemm_bias_gelu", kFnM4BiasGelu},
@@ -66,6 +67,7 @@ constexpr FnName kFunctions[] = {
     {"gemv_q8_qkv", kFnQkv},             {"logit_gemv_q8", kFnLogit},
     {"gpu_emb_lookup_q8", kFnEmbLookup}, {"emb_lookup_indirect_q8", kFnEmbIndirect},
     {"emb_pe_rows_q8", kFnEmbPeRows},    {"mul_mm_q8", kFnMulMmQ8},
+    {"m4_flash_enc", kFnFlashEnc},       {"flash_attention_enc_f16", kFnFlashEnc},
 };
 
 struct Deferred {

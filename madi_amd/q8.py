@@ -14,12 +14,13 @@ from dataclasses import dataclass
 
 import numpy as np
 
-from ._lib import EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RES, EPI_NONE, call, check, lib
+from ._lib import EPI_BIAS, EPI_BIAS_GELU, EPI_BIAS_RES, EPI_NONE, MadiError, call, check, lib
 
 D = 1280          # encoder.zig:12, decoder.zig:12
 MLP = 5120        # encoder.zig:15
 VOCAB = 51866     # decoder.zig:19
 ENC_SEQ = 1500    # encoder.zig:16
+NH = 20           # encoder.zig:13 (attention heads, head dim 64: encoder.zig:14)
 
 
 def ptr(t) -> int | None:
@@ -186,6 +187,16 @@ def kM4Bias(f, a, b, c, bias, m: int, n: int, k: int) -> None:
     call("madi_m4_gemm", _fn(f), ptr(a), ptr(b), ptr(c), ptr(bias), m, n, k)
 
 
+def kFlash(f, out, q, k, v, seq: int, nh: int = NH) -> None:
+    """encoder.zig:138-152: self-attention of one window over its Q, K, V
+    projections (f16 [seq][nh*64] each), f = the m4_flash_enc or
+    flash_attention_enc_f16 handle (or name); both run the same kernel."""
+    fid = _fn(f)
+    if fid not in (getFunction("m4_flash_enc"), getFunction("flash_attention_enc_f16")):
+        raise MadiError(-9, "kFlash", f"handle {fid} is not an encoder attention kernel")
+    call("madi_flash_enc_f16", ptr(out), ptr(q), ptr(k), ptr(v), seq, nh)
+
+
 def matmulF16Batched(a, b, c, m: int, n: int, k: int, alpha: float = 1.0,
                      beta: float = 0.0) -> None:
     """metal_backend.zig:120 -> mtl_matmul_f16_enc (metal_backend.h:103)."""
@@ -258,9 +269,9 @@ def gemv_f16x(out, x16, w: Q8, n: int, k: int, bias=None, epilogue: int = EPI_NO
 
 
 __all__ = [
-    "D", "MLP", "VOCAB", "ENC_SEQ", "Q8", "init", "sync", "getFunction", "materialize",
+    "D", "MLP", "VOCAB", "ENC_SEQ", "NH", "Q8", "init", "sync", "getFunction", "materialize",
     "set_deferred_dequant", "repack_host", "unpack_host",
-    "upload_q8", "upload_q8_device_repack", "quantize", "fnv", "FNV_SEED", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias", "kM4", "kM4Bias", "matmulF16Batched",
+    "upload_q8", "upload_q8_device_repack", "quantize", "fnv", "FNV_SEED", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias", "kM4", "kM4Bias", "kFlash", "matmulF16Batched",
     "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "pproj", "proj", "kQkv", "kLogitGemv", "embLookup",
     "embLookupIndirect", "prefillEmbed", "gemv_f16x", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU",
     "EPI_BIAS_RES",

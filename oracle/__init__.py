@@ -83,6 +83,7 @@ def _declare(L: ctypes.CDLL) -> None:
         "oracle_emb_row_q8": (None, [_P, _P, _P, _U32, _U32]),
         "oracle_emb_pe_rows_q8": (None, [_P, _P, _P, _P, _P, _U32, _U32, _U32]),
         "oracle_gemm_f16": (None, [_P, _P, _P, _U32, _U32, _U32, ctypes.c_float, ctypes.c_float, _I]),
+        "oracle_flash_enc_f16": (None, [_P, _P, _P, _P, _U32, _U32, _I]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -249,4 +250,15 @@ def gemm_f16(a, b, c=None, alpha=1.0, beta=0.0, threads=1):
     assert k == k2
     out = np.zeros((m, n), dtype=np.float16) if c is None else np.array(c, dtype=np.float16)
     lib().oracle_gemm_f16(_ptr(out), _ptr(a), _ptr(b), m, n, k, alpha, beta, threads)
+    return out
+
+
+def flash_enc_f16(q, k, v, nh: int, threads=1):
+    """m4_flash_enc (m4_gemm.metal:268-407): bidirectional attention with head
+    dim 64 over f16 [seq][nh*64] q, k, v; returns f16 [seq][nh*64]."""
+    q, k, v = _c(q, np.float16), _c(k, np.float16), _c(v, np.float16)
+    seq, width = q.shape
+    assert width == 64 * nh and k.shape == q.shape and v.shape == q.shape and seq >= 1
+    out = np.zeros((seq, width), dtype=np.float16)
+    lib().oracle_flash_enc_f16(_ptr(out), _ptr(q), _ptr(k), _ptr(v), seq, nh, threads)
     return out

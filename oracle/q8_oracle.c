@@ -308,3 +308,83 @@ void oracle_gemm_f16(uint16_t *c, const uint16_t *a, const uint16_t *b, uint32_t
       c[(size_t)mm * n + nn] = oracle_f32_to_f16(r);
     }
 }
+
+/* ---- encoder self-attention over the projections ---------------------------------
+ * m4_flash_enc (engine/metal/kernels/m4_gemm.metal:268-407), dispatched by kFlash
+ * (engine/metal/encoder.zig:138-152).  q, k, v, out: f16 [seq][nh*64], head hd in
+ * columns hd*64 .. hd*64+63.  Per head and 64-row query tile, over 64-key blocks
+ * (:325-400): S = Q.K^T in f32 (:327-336), v = S * 0.125 with keys >= seq at -inf
+ * (:342-356), the row max over the block's two 32-column halves and the running
+ * max m (:357-360), alpha = exp(m_old - m_new), 0 while m_old is -inf (:361),
+ * e = exp(v - m_new), masked keys 0 (:363-374), P = f16(e) (:375), per-half sums
+ * of the unrounded e folded as sum = sum * alpha + half0 + half1 (:377-382),
+ * O = O * alpha + P.V in f32 (:384-394); out = f16(O / (sum + 1e-6)) for rows
+ * < seq (:396-406).  Rows past seq and keys past seq are never read. */
+void oracle_flash_enc_f16(uint16_t *out, const uint16_t *q, const uint16_t *k,
+                          const uint16_t *v, uint32_t seq, uint32_t nh, int threads) {
+  if (threads < 1) threads = 1;
+  const uint32_t tiles = (seq + 63) / 64;
+  const size_t ld = (size_t)nh * 64;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+  for (uint32_t job = 0; job < nh * tiles; ++job) {
+    const uint32_t hd = job / tiles, q0 = (job % tiles) * 64;
+    const uint32_t rows = seq - q0 < 64 ? seq - q0 : 64;
+    float qf[64][64], o[64][64], s[64][64], m[64], sum[64];
+    uint16_t p[64][64];
+    for (uint32_t i = 0; i < rows; ++i) {
+      for (uint32_t d = 0; d < 64; ++d) {
+        qf[i][d] = oracle_f16_to_f32(q[(q0 + i) * ld + hd * 64 + d]);
+        o[i][d] = 0.0f;
+      }
+      m[i] = -INFINITY;
+      sum[i] = 0.0f;
+    }
+    for (uint32_t kv0 = 0; kv0 < seq; kv0 += 64) {
+      const uint32_t kcur = seq - kv0 < 64 ? seq - kv0 : 64;
+      for (uint32_t j = 0; j < kcur; ++j) {
+        float kr[64];
+        for (uint32_t d = 0; d < 64; ++d) kr[d] = oracle_f16_to_f32(k[(kv0 + j) * ld + hd * 64 + d]);
+        for (uint32_t i = 0; i < rows; ++i) {
+          float acc = 0.0f;
+          for (uint32_t d = 0; d < 64; ++d) acc += qf[i][d] * kr[d];
+          s[i][j] = acc;
+        }
+      }
+      for (uint32_t i = 0; i < rows; ++i) {
+        float half_max[2] = {-INFINITY, -INFINITY}, half_sum[2] = {0.0f, 0.0f};
+        for (uint32_t j = 0; j < kcur; ++j) {
+          const float x = s[i][j] * 0.125f;
+          if (x > half_max[j / 32]) half_max[j / 32] = x;
+        }
+        float m_new = m[i];
+        if (half_max[0] > m_new) m_new = half_max[0];
+        if (half_max[1] > m_new) m_new = half_max[1];
+        const float alpha = (m[i] == -INFINITY) ? 0.0f : expf(m[i] - m_new);
+        for (uint32_t hf = 0; hf < 2; ++hf)
+          for (uint32_t j4 = 32 * hf; j4 < 32 * hf + 32; j4 += 4) {
+            float e4[4];
+            for (uint32_t c = 0; c < 4; ++c) {
+              const uint32_t j = j4 + c;
+              e4[c] = j < kcur ? expf(s[i][j] * 0.125f - m_new) : 0.0f;
+              p[i][j] = oracle_f32_to_f16(e4[c]);
+            }
+            half_sum[hf] += e4[0] + e4[1] + e4[2] + e4[3];
+          }
+        m[i] = m_new;
+        sum[i] = sum[i] * alpha + half_sum[0] + half_sum[1];
+        for (uint32_t d = 0; d < 64; ++d) o[i][d] *= alpha;
+      }
+      for (uint32_t j = 0; j < kcur; ++j) {
+        float vr[64];
+        for (uint32_t d = 0; d < 64; ++d) vr[d] = oracle_f16_to_f32(v[(kv0 + j) * ld + hd * 64 + d]);
+        for (uint32_t i = 0; i < rows; ++i) {
+          const float pij = oracle_f16_to_f32(p[i][j]);
+          for (uint32_t d = 0; d < 64; ++d) o[i][d] += pij * vr[d];
+        }
+      }
+    }
+    for (uint32_t i = 0; i < rows; ++i)
+      for (uint32_t d = 0; d < 64; ++d)
+        out[(q0 + i) * ld + hd * 64 + d] = oracle_f32_to_f16(o[i][d] / (sum[i] + 1e-6f));
+  }
+}

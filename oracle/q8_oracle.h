@@ -25,6 +25,11 @@
  *   quantize .................... round-half-away knife edges, |q|<=127,
  *                                 block max maps to 127, all-zero block -> 1.0
  *   fnv1a64 ..................... published FNV-1a 64-bit test vectors
+ *   flash_enc ................... fp64 softmax attention within the bound the
+ *                                 f16 rounding of P allows, uniform attention
+ *                                 (q = 0) = mean of the value rows, one-hot
+ *                                 peaked attention, key-order and head
+ *                                 independence, planted-mistake mutants
  */
 #ifndef MADI_Q8_ORACLE_H
 #define MADI_Q8_ORACLE_H
@@ -89,6 +94,11 @@ void oracle_emb_pe_rows_q8(float *out, const int8_t *qs, const uint16_t *scales,
 
 void oracle_gemm_f16(uint16_t *c, const uint16_t *a, const uint16_t *b, uint32_t m,
                      uint32_t n, uint32_t k, float alpha, float beta, int threads);
+
+/* m4_gemm.metal:268-407 m4_flash_enc: bidirectional attention, head dim 64, over
+ * q, k, v f16 [seq][nh*64] (head hd in columns hd*64..), f16 out of the same shape. */
+void oracle_flash_enc_f16(uint16_t *out, const uint16_t *q, const uint16_t *k,
+                          const uint16_t *v, uint32_t seq, uint32_t nh, int threads);
 
 #ifdef __cplusplus
 }

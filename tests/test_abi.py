@@ -46,7 +46,7 @@ FAKE = 0x100000  # 16-byte aligned, never dereferenced: every call below fails v
 HANDLE_NAMES = ["dequant_q8_f16", "m4_gemm_nn", "m4_gemm_bias", "m4_gemm_bias_gelu", "gemv_q8",
                 "gemv_q8_bias", "gemv_q8_bias_gelu", "gemv_q8_bias_res", "gemv_q8_qkv",
                 "logit_gemv_q8", "gpu_emb_lookup_q8", "emb_lookup_indirect_q8", "emb_pe_rows_q8",
-                "mul_mm_q8"]
+                "mul_mm_q8", "m4_flash_enc"]
 
 
 def test_function_handles_by_name():
@@ -61,6 +61,8 @@ def test_function_handles_by_name():
     assert L.madi_m4_gemm(ids["gemv_q8"], FAKE, FAKE, FAKE, None, 16, 256, 1280) == -9
     assert L.madi_q8_gemv_epi(ids["m4_gemm_bias"], FAKE, FAKE, FAKE, FAKE, FAKE, 256, 1280) == -9
     assert L.madi_m4_gemm(ids["m4_gemm_nn"], FAKE, FAKE, FAKE, None, 16, 256, 1280) == -8
+    # the reference's two encoder attention kernels compute the same thing: one handle
+    assert q8.getFunction("flash_attention_enc_f16") == ids["m4_flash_enc"]
 
 
 @pytest.mark.parametrize("call,args,code", [
@@ -96,6 +98,13 @@ def test_function_handles_by_name():
     ("madi_q8_pproj", (FAKE, None, FAKE, FAKE, 8, 1280, 1280), -6),
     ("madi_q8_pproj", (FAKE, FAKE + 4, FAKE, FAKE, 8, 1280, 1280), -7),
     ("madi_q8_pproj", (FAKE, FAKE, FAKE, FAKE, 65535 * 32, 32, 64), -8),         # largest M, not initialised
+    ("madi_flash_enc_f16", (FAKE, FAKE + 0x10000, None, FAKE + 0x30000, 1500, 20), -6),
+    ("madi_flash_enc_f16", (FAKE, FAKE + 0x1000000, FAKE + 0x2000000, FAKE + 0x3000000, 1500, 0), -5),
+    ("madi_flash_enc_f16", (FAKE, FAKE, FAKE, FAKE, 1 << 21, 16), -5),            # > 2 GiB
+    ("madi_flash_enc_f16", (FAKE, FAKE + 0x1000000, FAKE + 0x2000008, FAKE + 0x3000000, 1500, 20), -7),
+    ("madi_flash_enc_f16", (FAKE, FAKE + 0x1000000, FAKE + 0x100000, FAKE + 0x3000000, 1500, 20), -9),  # out over k
+    ("madi_flash_enc_f16", (FAKE, FAKE + 0x100, FAKE + 0x2000000, FAKE + 0x3000000, 1500, 20), -9),  # out over q
+    ("madi_flash_enc_f16", (FAKE, FAKE, FAKE + 0x2000000, FAKE + 0x3000000, 1500, 20), -8),  # in place on q
     ("madi_alloc", (16,), None),
     ("madi_sync", (), -8),
     ("madi_upload", (FAKE, FAKE, 16), -8),

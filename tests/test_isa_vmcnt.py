@@ -58,6 +58,30 @@ def test_every_persistent_instance_is_race_free(gemm_asm):
     assert not bad, bad
 
 
+@pytest.fixture(scope="module")
+def attn_asm(tmp_path_factory):
+    if not shutil.which(HIPCC) and not os.path.exists(HIPCC):
+        pytest.skip("hipcc not available")
+    from madi_amd.build import HIP_FLAGS
+    out = tmp_path_factory.mktemp("isa") / "attn.s"
+    src = os.path.join(ROOT, "madi_amd", "csrc", "attn.hip")
+    flags = [f for f in HIP_FLAGS if f != "-fPIC"]
+    subprocess.run([HIPCC, *flags, "--cuda-device-only", "-S", src, "-o", str(out)],
+                   check=True, capture_output=True)
+    return kernels(out.read_text())
+
+
+def test_every_attention_instance_is_race_free(attn_asm):
+    """The encoder attention kernel (one and two key groups): the Q fragments
+    loaded into registers are not touched before their wait, on any of the
+    prologue's paths, and the block loop adds no register loads."""
+    names = [n for n in attn_asm if "flash_enc_kernel" in n]
+    assert len(names) == 2, names
+    bad = {n: hazards(attn_asm[n])[:3] for n in names}
+    bad = {n: b for n, b in bad.items() if b}
+    assert not bad, bad
+
+
 def test_checker_catches_a_premature_read():
     """The checker itself: a read of a load's destination before its wait,
     and a register reused while a dead load is in flight, are both flagged;
