@@ -22,9 +22,11 @@ encoder GEMM set of one 30 s window (32 layers, independent weights), a
 batched decode step at M = 8 and 16 (skinny Q8 projections, cold weights) with
 the per-chunk cross-attention K|V GEMM, one decoder token at M = 1 through the
 GEMV family (and its fused q|k|v GEMV alone), one decoder layer's sequence
-prefill projections at M = 320, and the 16-window long-audio fc1/fc2.
+prefill projections at M = 320, the 16-window long-audio fc1/fc2, and the
+encoder self-attention of one window over its Q/K/V projections.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-configs]
+       python bench.py --config NAME     (one configuration alone, e.g. encoder_attention)
        python bench.py --calibrate-copy   (a plain 256 MiB device copy, the
                                            reference kernel for FETCH_SIZE /
                                            WRITE_SIZE scaling)
@@ -408,6 +410,38 @@ def cpu_model():
     return "unknown"
 
 
+def config_encoder_attention(torch, stream, q8, reps=50):
+    """The encoder self-attention of one 30 s window over its Q, K, V
+    projections (the kFlash call, engine/metal/encoder.zig:138-152): 1500
+    frames x 20 heads x head dim 64, f16, one layer.  FLOPs = 4 seq^2 64 heads
+    (Q K^T and P V; the softmax is not counted), against the fp16 MFMA peak."""
+    seq, nh = q8.ENC_SEQ, q8.NH
+    g = torch.Generator(device="cuda").manual_seed(200)
+    q, k, v = (torch.randn(seq, nh * 64, device="cuda", generator=g).half() for _ in range(3))
+    o = torch.empty_like(q)
+    f = q8.getFunction("m4_flash_enc")
+
+    def one(_):
+        q8.kFlash(f, o, q, k, v, seq, nh)
+
+    one(0)
+    t = _timed(torch, stream, one, reps)
+    flops = 4.0 * seq * seq * 64 * nh
+    return {
+        "workload": "encoder self-attention, 1500 frames x 20 heads x 64, f16 Q/K/V/out, one layer",
+        "us": round(t * 1e6, 2), "gflop": round(flops / 1e9, 3),
+        "tflops": round(flops / t / 1e12, 1),
+        "frac_fp16_peak": round(flops / t / 1e12 / PEAK_FP16_TFLOPS, 4),
+    }
+
+
+CONFIGS = {
+    "encoder_window": config_encoder_window, "batched_decode": config_batched_decode,
+    "decode_token": config_decode_token, "prefill": config_prefill,
+    "long_audio": config_long_audio, "encoder_attention": config_encoder_attention,
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -419,6 +453,9 @@ def main():
                          "measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy (PMC calibration)")
+    ap.add_argument("--config", choices=sorted(CONFIGS),
+                    help="only run this one configuration and print its JSON (for profiling "
+                         "one workload's kernels)")
     args = ap.parse_args()
     if args.calibrate_copy:
         calibrate_copy()
@@ -437,6 +474,11 @@ def main():
     stream = torch.cuda.current_stream()
     q8.init(stream)
     dev_name = torch.cuda.get_device_name(0)
+    if args.config:
+        log(f"device {dev_name}; configuration {args.config} only")
+        print(json.dumps({"config": args.config, "device": dev_name,
+                          **CONFIGS[args.config](torch, stream, q8)}))
+        return
     log(f"device {dev_name}; preparing inputs")
 
     a, qs, sc = synth.gemm_case(0, M, N, K)
@@ -547,6 +589,8 @@ def main():
         cfg["prefill"] = config_prefill(torch, stream, q8)
         log("long audio (M=24000)")
         cfg["long_audio"] = config_long_audio(torch, stream, q8)
+        log("encoder self-attention (1500 x 20 heads)")
+        cfg["encoder_attention"] = config_encoder_attention(torch, stream, q8)
         result["configs"] = cfg
     if not args.no_cpu:
         threads = cpu_share()

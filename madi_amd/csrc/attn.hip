@@ -5,12 +5,14 @@
 //
 // Arithmetic, as the reference's: S = Q K^T in f32 from f16 operands, scaled
 // by 1/8; an online softmax over 64-key blocks against a running row max;
-// P = f16(e); O += P V in f32; out = f16(O / (sum + 1e-6)).  Two changes that
-// move only roundings: e is the hardware exp2 of s * log2(e)/8 - m', and the
+// P = f16(e); O += P V in f32; out = f16(O / (sum + 1e-6)).  Three changes
+// that move only roundings: e is the hardware exp2 of s * log2(e)/8 - m'; the
 // reference max m' is raised only when a block's max passes it by more than 8
 // (log2 units), so e <= 256 (well inside f16, each P still rounded relative to
 // its own magnitude) and O and the sum are rescaled in a few blocks instead of
-// in every block.  The sum adds the unrounded e, as the reference's does.
+// in every block; and the sum adds the rounded P (v_dot2_f32_f16, half the
+// instructions of adding the f32 e), so out is a weighted mean of the V rows
+// with exactly the weights the product used.
 //
 // Layout: q, k, v, out f16 [seq][nh*64], head hd in columns 64hd..64hd+63 (the
 // projection GEMMs' output, unpadded: rows past seq are never read -- row
@@ -31,8 +33,12 @@
 //     the LDS transpose read (ds_read_b64_tr_b16: 16 lanes pass 4 rows x 16
 //     columns of f16, lane c receives column c), which gives each lane one d
 //     and four consecutive keys.
+// Per block the matrix cores take the next block's S^T and this block's
+// O^T += V^T P^T while the VALU computes this block's softmax: the exponentials
+// of each group of 8 scores feed two P V products at once, between which two
+// of the next block's S products run.
 // The K and V tiles of a block (64 rows x 128 bytes each) arrive by LDS DMA in
-// a 3-stage ring per key group, two blocks ahead, with one barrier per block;
+// a 4-stage ring per key group, three blocks ahead, with one barrier per block;
 // the 16-byte pieces of each row are XOR-swizzled so that the K fragment reads
 // (32 rows, one piece each) and the transpose reads (8 rows x 64 bytes) spread
 // over all banks.
@@ -46,7 +52,7 @@ namespace {
 constexpr int kQRows = 128;                        // query rows per workgroup
 constexpr int kTileBytes = 64 * 64 * 2;            // one K or V tile: 64 keys x 64 d
 constexpr int kStageBytes = 2 * kTileBytes;        // K tile, then V tile
-constexpr int kRingBytes = 3 * kStageBytes;        // per key group
+constexpr int kRingBytes = 4 * kStageBytes;        // per key group
 constexpr float kScaleLog2 = 0.125f * 1.4426950408889634f;  // 1/8 * log2(e)
 constexpr float kLazy = 8.0f;  // raise the reference max when exceeded by more than this
 
@@ -125,38 +131,38 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
   // DMA plan: wave wq copies rows 16wq .. 16wq+15 of the K and V tiles, 8 rows
   // per DMA; lane -> row 16wq + 8i + lane/8, LDS piece lane%8, which holds the
   // row's logical piece (lane%8) ^ swizzle(row)
-  uint32_t drow[2], kpiece[2], vpiece[2];
+  uint32_t k_dma[2], v_dma[2], drow[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     drow[i] = 16 * wq + 8 * i + (lane >> 3);
-    kpiece[i] = head * 128 + 16 * ((lane & 7) ^ swz_k(drow[i]));
-    vpiece[i] = head * 128 + 16 * ((lane & 7) ^ swz_v(drow[i]));
+    k_dma[i] = head * 128 + 16 * ((lane & 7) ^ swz_k(drow[i]));
+    v_dma[i] = head * 128 + 16 * ((lane & 7) ^ swz_v(drow[i]));
   }
   auto issue = [&](uint32_t blk, uint32_t stage) {
     const uint32_t kv0 = (kb0 + blk) * 64;
     const uint32_t kt = ring + stage * kStageBytes + 16 * wq * 128;
+    if (kv0 + 64 <= seq) {  // a whole block: the block offset is a scalar
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const uint32_t row = min(kv0 + drow[i], seq - 1) * rowb;
-      dma16<0, true>(dk, row + kpiece[i], 0, kt + i * 1024);
-      dma16<0, true>(dv, row + vpiece[i], 0, kt + kTileBytes + i * 1024);
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t row = drow[i] * rowb;
+        dma16<0, true>(dk, row + k_dma[i], kv0 * rowb, kt + i * 1024);
+        dma16<0, true>(dv, row + v_dma[i], kv0 * rowb, kt + kTileBytes + i * 1024);
+      }
+    } else {  // the last block: rows past seq repeat the last row
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const uint32_t row = min(kv0 + drow[i], seq - 1) * rowb;
+        dma16<0, true>(dk, row + k_dma[i], 0, kt + i * 1024);
+        dma16<0, true>(dv, row + v_dma[i], 0, kt + kTileBytes + i * 1024);
+      }
     }
   };
-  if (nblk > 0) issue(0, 0);
-  if (nblk > 1) issue(1, 1);
-  // one unconditional wait for Q and both first blocks: the fragments pass
-  // through a single asm statement, so the compiler has no merged copy of
-  // them to make before the wait
-  wait_q_then_barrier(qf);
-  f16x8 qh[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) qh[s] = __builtin_bit_cast(f16x8, qf[s]);
-
   // lane constants of the fragment reads: K row r at piece 2s + h; V^T via
   // transpose reads: lane (g = lane/16, c = lane%16) passes row 4h + c/4 of a
   // 4-row group, columns 32dd + 16(g%2) + 4(c%4) .. +3
-  const uint32_t k_row = r * 128, k_swz = swz_k(r);
-  uint32_t v_off[2];
+  uint32_t k_off[4], v_off[2];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) k_off[st] = r * 128 + 16 * ((2 * st + h) ^ swz_k(r));
   {
     const uint32_t c = lane & 15, rr = c >> 2, cc = c & 3;
     const uint32_t vrow = 4 * h + rr;
@@ -166,25 +172,69 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
       v_off[dd] = vrow * 128 + 16 * (piece ^ swz_v(vrow)) + 8 * (cc & 1);
     }
   }
+  auto read_k = [&](uint32_t kt, f16x8(&kf)[2][4]) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int st = 0; st < 4; ++st) kf[t][st] = lds_read16(kt + k_off[st] + t * 32 * 128);
+  };
+  // One block's fragments in the order the group loop consumes them: for
+  // group (t, a) the two K fragments of its S products (next block) and the
+  // two V^T fragments of its P V products (this block).
+  auto read_frags = [&](uint32_t kt, uint32_t vt, f16x8(&kf)[2][4], f16x8(&vf)[2][2][2]) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int t = g >> 1, a = g & 1;
+      kf[t][2 * a] = lds_read16(kt + k_off[2 * a] + t * 32 * 128);
+      kf[t][2 * a + 1] = lds_read16(kt + k_off[2 * a + 1] + t * 32 * 128);
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd) {
+        const uint32_t at = vt + v_off[dd] + (32 * t + 16 * a) * 128;
+        const f16x4 lo = lds_read_tr(at), hi = lds_read_tr(at + 8 * 128);
+        vf[dd][t][a] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    }
+  };
 
+  // Prologue: Q and blocks 0 and 1 resident, block 2 on its way, S of block 0.
+  if (nblk > 0) issue(0, 0);
+  if (nblk > 1) issue(1, 1);
+  // one unconditional wait for Q and both first blocks: the fragments pass
+  // through a single asm statement, so the compiler has no merged copy of
+  // them to make before the wait
+  wait_q_then_barrier(qf);
+  if (nblk > 2) issue(2, 2);
+  f16x8 qh[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) qh[st] = __builtin_bit_cast(f16x8, qf[st]);
+  f32x16 s[2] = {};
+  if (nblk > 0) {
+    f16x8 kf[2][4];
+    read_k(ring, kf);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+        s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][st], qh[st], s[t], 0, 0, 0);
+  }
+
+  // Block j: its softmax on the VALU while the matrix cores take the next
+  // block's S and this block's P V, interleaved group by group.  The loop
+  // keeps blocks j + 1 (its K is read here) and j + 2 resident and block j + 3
+  // in flight.
   f32x16 o[2] = {};
   float mref = -__builtin_inff(), l = 0.0f;
-  uint32_t stage = 0;
-  for (uint32_t j = 0; j < iters; ++j) {
-    if (j + 2 < nblk) issue(j + 2, stage == 0 ? 2 : stage - 1);
+  const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+  // one block: s holds its S^T, sn receives the next block's
+  auto step = [&](uint32_t j, uint32_t stage, f32x16(&s)[2], f32x16(&sn)[2]) {
+    if (j + 3 < nblk) issue(j + 3, (stage + 3) & 3);
     if (j < nblk) {
-      const uint32_t kt = ring + stage * kStageBytes, vt = kt + kTileBytes;
+      const uint32_t cur = ring + stage * kStageBytes;
+      // the next block's K (this block's when there is none: multiplied, unused)
+      const uint32_t nxt = j + 1 < nblk ? ring + ((stage + 1) & 3) * kStageBytes : cur;
+      f16x8 kf[2][4], vf[2][2][2];
+      read_frags(nxt, cur + kTileBytes, kf, vf);
       const uint32_t kv0 = (kb0 + j) * 64;
-      f32x16 s[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        s[t] = (f32x16){};
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const f16x8 kf = lds_read16(kt + t * 32 * 128 + k_row + 16 * ((2 * st + h) ^ k_swz));
-          s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qh[st], s[t], 0, 0, 0);
-        }
-      }
       if (kv0 + 64 > seq) {  // the last block: keys past seq take no weight
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -192,16 +242,19 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
           for (int e = 0; e < 16; ++e)
             if (kv0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3) >= seq) s[t][e] = -__builtin_inff();
       }
+      // Each lane tests its own 32 scores against the reference max; only
+      // when some lane's pass it does the wave take the two halves' common
+      // max (the two halves of a query must keep one reference), so the
+      // usual block has no cross-lane step ahead of its exponentials.
       float mx = s[0][0];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int e = 0; e < 16; ++e) mx = __builtin_fmaxf(mx, s[t][e]);
-      mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = mx * kScaleLog2;
-      const bool up = mnew > mref + kLazy;
-      if (__builtin_amdgcn_ballot_w64(up)) {
-        const float nref = up ? mnew : mref;
+      if (__builtin_amdgcn_ballot_w64(mx * kScaleLog2 > mref + kLazy)) {
+        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+        const float mnew = mx * kScaleLog2;
+        const float nref = mnew > mref + kLazy ? mnew : mref;
         const float alpha = __builtin_amdgcn_exp2f(mref - nref);  // 0 on the first block
         l *= alpha;
 #pragma unroll
@@ -211,39 +264,42 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
         mref = nref;
       }
       const float nm = -mref;
-      f16x8 p[2][2];
-      float ls[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      // four groups of 8 scores (t, a): their exponentials and P, the two
+      // P V products of the group, and two of the next block's S products
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int g = 0; g < 4; ++g) {
+        const int t = g >> 1, a = g & 1;
+        f16x8 p;
 #pragma unroll
-        for (int a = 0; a < 2; ++a)
+        for (int e = 0; e < 8; ++e)
+          p[e] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * a + e], kScaleLog2, nm));
+        // the row sum adds the rounded weights, so out is a weighted mean of V
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float ex = __builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * a + e], kScaleLog2, nm));
-            ls[e & 3] += ex;
-            p[t][a][e] = (f16)ex;
-          }
-      l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
-#pragma unroll
-      for (int dd = 0; dd < 2; ++dd)
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int a = 0; a < 2; ++a) {
-            const uint32_t base = vt + (32 * t + 16 * a) * 128 + v_off[dd];
-            const f16x4 lo = lds_read_tr(base), hi = lds_read_tr(base + 8 * 128);
-            const f16x8 vf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-            o[dd] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, p[t][a], o[dd], 0, 0, 0);
-          }
+        for (int e = 0; e < 8; e += 2)
+          l = __builtin_amdgcn_fdot2((f16x2){p[e], p[e + 1]}, ones, l, false);
+        o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[0][t][a], p, o[0], 0, 0, 0);
+        o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[1][t][a], p, o[1], 0, 0, 0);
+        sn[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][2 * a], qh[2 * a],
+                                                       a ? sn[t] : (f32x16){}, 0, 0, 0);
+        sn[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][2 * a + 1], qh[2 * a + 1], sn[t], 0, 0, 0);
+      }
     }
-    // block j + 1 has landed (block j + 2's DMAs may be in flight) and every
-    // wave is done with block j's stage
-    if (j + 2 < nblk)
+    // block j + 2 has landed (block j + 3's DMAs may be in flight) and every
+    // wave is done with block j's stage and block j + 1's K
+    if (j + 3 < nblk)
       wait_then_barrier<4>();
     else
       wait_then_barrier<0>();
-    stage = stage == 2 ? 0 : stage + 1;
+  };
+  // two blocks per trip, the S buffers trading roles, so no copy between them
+  f32x16 s2[2];
+  uint32_t j = 0, stage = 0;
+  for (; j + 2 <= iters; j += 2, stage = (stage + 2) & 3) {
+    step(j, stage, s, s2);
+    step(j + 1, (stage + 1) & 3, s2, s);
   }
+  if (j < iters) step(j, stage, s, s2);
+
   // each lane summed the weights of its own 32 keys per block; the two lane
   // halves share the reference max, so their sums add
   l += __shfl_xor(l, 32);

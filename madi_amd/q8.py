@@ -191,10 +191,16 @@ def kFlash(f, out, q, k, v, seq: int, nh: int = NH) -> None:
     """encoder.zig:138-152: self-attention of one window over its Q, K, V
     projections (f16 [seq][nh*64] each), f = the m4_flash_enc or
     flash_attention_enc_f16 handle (or name); both run the same kernel."""
+    global _FLASH_IDS
+    if _FLASH_IDS is None:
+        _FLASH_IDS = (getFunction("m4_flash_enc"), getFunction("flash_attention_enc_f16"))
     fid = _fn(f)
-    if fid not in (getFunction("m4_flash_enc"), getFunction("flash_attention_enc_f16")):
+    if fid not in _FLASH_IDS:
         raise MadiError(-9, "kFlash", f"handle {fid} is not an encoder attention kernel")
     call("madi_flash_enc_f16", ptr(out), ptr(q), ptr(k), ptr(v), seq, nh)
+
+
+_FLASH_IDS = None
 
 
 def matmulF16Batched(a, b, c, m: int, n: int, k: int, alpha: float = 1.0,
