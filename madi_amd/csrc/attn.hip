@@ -18,11 +18,12 @@
 // projection GEMMs' output, unpadded: rows past seq are never read -- row
 // indices clamp to the last row, and the keys past seq get weight 0).
 //
-// Workgroup: 128 query rows of one head.  A key group of 4 waves walks the
-// keys; wave w owns query rows 32w..32w+31 (the MFMA's 32 columns).  KS = 2
-// splits the key range between two such groups (two waves per SIMD, whose
-// matrix and vector work interleave); their partial (m', sum, O) meet in LDS
-// at the end.  Per 64-key block a wave computes
+// Workgroup: 128 query rows of one head.  A key group of 4 waves walks a
+// range of the keys; wave w owns query rows 32w..32w+31 (the MFMA's 32
+// columns).  KS key groups (KS waves per SIMD) split the key range and merge
+// their partial (m', sum, O) in LDS at the end; the default is four, whose
+// waves overlap each other's matrix and vector work.  Per 64-key block a
+// wave computes
 //   S^T = K Q^T: two v_mfma_f32_32x32x16_f16 tiles with the keys as rows, so
 //     lane (h, r) holds query r's scores of keys 32t + 8j + 4h + i
 //     (s[t][4j + i]): row max and sum are in-lane plus one exchange between
@@ -33,15 +34,15 @@
 //     the LDS transpose read (ds_read_b64_tr_b16: 16 lanes pass 4 rows x 16
 //     columns of f16, lane c receives column c), which gives each lane one d
 //     and four consecutive keys.
-// Per block the matrix cores take the next block's S^T and this block's
-// O^T += V^T P^T while the VALU computes this block's softmax: the exponentials
-// of each group of 8 scores feed two P V products at once, between which two
-// of the next block's S products run.
 // The K and V tiles of a block (64 rows x 128 bytes each) arrive by LDS DMA in
-// a 4-stage ring per key group, three blocks ahead, with one barrier per block;
-// the 16-byte pieces of each row are XOR-swizzled so that the K fragment reads
-// (32 rows, one piece each) and the transpose reads (8 rows x 64 bytes) spread
-// over all banks.
+// a ring per key group, one barrier per block; the 16-byte pieces of each row
+// are XOR-swizzled so that the K fragment reads (32 rows, one piece each) and
+// the transpose reads (8 rows x 64 bytes) spread over all banks.  Two
+// schedules: the plain one (three or four key groups: S at the start of each
+// block, a 3- or 2-stage ring), and a pipelined one for one or two groups
+// (the next block's S on the matrix cores during this block's softmax, the
+// exponentials of each group of 8 scores feeding two P V products with two
+// S products between them; a 4-stage ring, three blocks ahead).
 #include "common.h"
 #include "vmem.h"
 
@@ -52,7 +53,14 @@ namespace {
 constexpr int kQRows = 128;                        // query rows per workgroup
 constexpr int kTileBytes = 64 * 64 * 2;            // one K or V tile: 64 keys x 64 d
 constexpr int kStageBytes = 2 * kTileBytes;        // K tile, then V tile
-constexpr int kRingBytes = 4 * kStageBytes;        // per key group
+// Ring stages per key group: four for the pipelined schedule (blocks j+1
+// and j+2 resident and j+3 in flight while block j computes), three or two
+// for the plain schedule of three or four key groups (blocks j+1, j+2 or
+// only j+1 in flight), which must fit 160 KiB of LDS for all groups.
+template <int KS, bool PIPE>
+constexpr int kStages = PIPE ? 4 : (KS >= 4 ? 2 : 3);
+template <int KS, bool PIPE>
+constexpr int kRingBytes = kStages<KS, PIPE> * kStageBytes;  // per key group
 constexpr float kScaleLog2 = 0.125f * 1.4426950408889634f;  // 1/8 * log2(e)
 constexpr float kLazy = 8.0f;  // raise the reference max when exceeded by more than this
 
@@ -82,12 +90,19 @@ __device__ inline void wait_q_then_barrier(u32x4 (&qf)[4]) {
                : "memory");
 }
 
-// Grid: one workgroup per (head, 128-row query tile), 256 * KS threads.
-template <int KS>
+// Grid: one workgroup per (head, 128-row query tile), 256 * KS threads: KS
+// key groups of four waves.  PIPE: the next block's S during this block's
+// softmax (two key groups, two waves per SIMD); otherwise S at the start of
+// each block and the three or four waves per SIMD overlap each other.
+template <int KS, bool PIPE>
 __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
     f16 *__restrict__ out, const f16 *__restrict__ q, const f16 *__restrict__ k,
     const f16 *__restrict__ v, uint32_t seq, uint32_t nh, uint32_t qtiles) {
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[KS * kRingBytes];
+  constexpr int NS = kStages<KS, PIPE>;
+  constexpr int RB = kRingBytes<KS, PIPE>;
+  static_assert(KS * RB <= 160 * 1024, "LDS");
+  static_assert((KS - 1) * 4 * 34 * 64 * 4 <= KS * RB, "exchange area");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[KS * RB];
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = sgpr(threadIdx.x >> 6);
   const uint32_t grp = wave >> 2, wq = wave & 3;
@@ -117,16 +132,14 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
     vload16<96>(qf[3], dq, qv, 0);
   }
 
-  // key blocks of this wave's group
+  // key blocks of this wave's group: group g takes blocks [g nb / KS,
+  // (g+1) nb / KS); every group runs the same number of loop trips (one
+  // barrier each), the largest group's count
   const uint32_t nb = (seq + 63) >> 6;
-  uint32_t kb0 = 0, nblk = nb, iters = nb;
-  if constexpr (KS == 2) {
-    const uint32_t nb0 = (nb + 1) >> 1;
-    kb0 = grp ? nb0 : 0;
-    nblk = grp ? nb - nb0 : nb0;
-    iters = nb0;
-  }
-  const uint32_t ring = lds_addr(smem) + grp * kRingBytes;
+  const uint32_t kb0 = grp * nb / KS;
+  const uint32_t nblk = (grp + 1) * nb / KS - kb0;
+  const uint32_t iters = (nb + KS - 1) / KS;
+  const uint32_t ring = lds_addr(smem) + grp * RB;
 
   // DMA plan: wave wq copies rows 16wq .. 16wq+15 of the K and V tiles, 8 rows
   // per DMA; lane -> row 16wq + 8i + lane/8, LDS piece lane%8, which holds the
@@ -196,7 +209,123 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
     }
   };
 
-  // Prologue: Q and blocks 0 and 1 resident, block 2 on its way, S of block 0.
+  f32x16 o[2] = {};
+  float mref = -__builtin_inff(), l = 0.0f;
+  const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+  // The last block's keys past seq take no weight; then the reference max:
+  // each lane tests its own 32 scores against it, and only when some lane's
+  // pass it does the wave take the two halves' common max (the two halves of
+  // a query must keep one reference), so the usual block has no cross-lane
+  // step ahead of its exponentials.
+  auto prep = [&](uint32_t kv0, f32x16(&s)[2]) {
+    if (kv0 + 64 > seq) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+          if (kv0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3) >= seq) s[t][e] = -__builtin_inff();
+    }
+    float mx = s[0][0];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = __builtin_fmaxf(mx, s[t][e]);
+    if (__builtin_amdgcn_ballot_w64(mx * kScaleLog2 > mref + kLazy)) {
+      mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = mx * kScaleLog2;
+      const float nref = mnew > mref + kLazy ? mnew : mref;
+      const float alpha = __builtin_amdgcn_exp2f(mref - nref);  // 0 on the first block
+      l *= alpha;
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dd][e] *= alpha;
+      mref = nref;
+    }
+  };
+  // group g = (t, a) of 8 scores: exponentials and P (f16), the row sum over
+  // the rounded P (so out is a weighted mean of the V rows with exactly the
+  // weights the product used)
+  auto exps = [&](const f32x16(&s)[2], int g) {
+    const int t = g >> 1, a = g & 1;
+    const float nm = -mref;
+    f16x8 p;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      p[e] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * a + e], kScaleLog2, nm));
+#pragma unroll
+    for (int e = 0; e < 8; e += 2) l = __builtin_amdgcn_fdot2((f16x2){p[e], p[e + 1]}, ones, l, false);
+    return p;
+  };
+
+  if constexpr (!PIPE) {
+    // Plain schedule.  Prologue: Q and the first NS - 1 blocks resident.
+#pragma unroll
+    for (int i = 0; i < NS - 1; ++i)
+      if (nblk > (uint32_t)i) issue(i, i);
+    wait_q_then_barrier(qf);
+    f16x8 qh[4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) qh[st] = __builtin_bit_cast(f16x8, qf[st]);
+    uint32_t stage = 0;
+    for (uint32_t j = 0; j < iters; ++j) {
+      if (j + NS - 1 < nblk) issue(j + NS - 1, stage == 0 ? NS - 1 : stage - 1);
+      if (j < nblk) {
+        const uint32_t cur = ring + stage * kStageBytes;
+        f32x16 s[2];
+        {
+          f16x8 kf[2][4];
+          read_k(cur, kf);
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][0], qh[0], (f32x16){}, 0, 0, 0);
+#pragma unroll
+            for (int st = 1; st < 4; ++st)
+              s[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][st], qh[st], s[t], 0, 0, 0);
+          }
+        }
+        // V^T fragments of group g (t, a) for d tile dd
+        auto read_v = [&](int g, int dd) {
+          const uint32_t at = cur + kTileBytes + v_off[dd] + (32 * (g >> 1) + 16 * (g & 1)) * 128;
+          const f16x4 lo = lds_read_tr(at), hi = lds_read_tr(at + 8 * 128);
+          return (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        };
+        // three groups: all sixteen fragments up front (the reads overlap the
+        // max); four groups (128 VGPRs per wave): each softmax group's own
+        f16x8 vf[4][2];
+        if constexpr (KS < 4) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int dd = 0; dd < 2; ++dd) vf[g][dd] = read_v(g, dd);
+        }
+        prep((kb0 + j) * 64, s);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          if constexpr (KS >= 4) {
+            vf[g][0] = read_v(g, 0);
+            vf[g][1] = read_v(g, 1);
+          }
+          const f16x8 p = exps(s, g);
+          o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[g][0], p, o[0], 0, 0, 0);
+          o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[g][1], p, o[1], 0, 0, 0);
+        }
+      }
+      // block j + 1 has landed (later blocks' DMAs may be in flight) and
+      // every wave is done with block j's stage
+      if constexpr (NS == 3) {
+        if (j + 2 < nblk)
+          wait_then_barrier<4>();
+        else
+          wait_then_barrier<0>();
+      } else {
+        wait_then_barrier<0>();
+      }
+      stage = stage + 1 == NS ? 0 : stage + 1;
+    }
+  } else {
+    // Pipelined schedule.  Prologue: Q and blocks 0 and 1 resident, block 2
+    // on its way, S of block 0.
   if (nblk > 0) issue(0, 0);
   if (nblk > 1) issue(1, 1);
   // one unconditional wait for Q and both first blocks: the fragments pass
@@ -222,9 +351,6 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
   // block's S and this block's P V, interleaved group by group.  The loop
   // keeps blocks j + 1 (its K is read here) and j + 2 resident and block j + 3
   // in flight.
-  f32x16 o[2] = {};
-  float mref = -__builtin_inff(), l = 0.0f;
-  const f16x2 ones = {(f16)1.0f, (f16)1.0f};
   // one block: s holds its S^T, sn receives the next block's
   auto step = [&](uint32_t j, uint32_t stage, f32x16(&s)[2], f32x16(&sn)[2]) {
     if (j + 3 < nblk) issue(j + 3, (stage + 3) & 3);
@@ -234,49 +360,13 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
       const uint32_t nxt = j + 1 < nblk ? ring + ((stage + 1) & 3) * kStageBytes : cur;
       f16x8 kf[2][4], vf[2][2][2];
       read_frags(nxt, cur + kTileBytes, kf, vf);
-      const uint32_t kv0 = (kb0 + j) * 64;
-      if (kv0 + 64 > seq) {  // the last block: keys past seq take no weight
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int e = 0; e < 16; ++e)
-            if (kv0 + 32 * t + 8 * (e >> 2) + 4 * h + (e & 3) >= seq) s[t][e] = -__builtin_inff();
-      }
-      // Each lane tests its own 32 scores against the reference max; only
-      // when some lane's pass it does the wave take the two halves' common
-      // max (the two halves of a query must keep one reference), so the
-      // usual block has no cross-lane step ahead of its exponentials.
-      float mx = s[0][0];
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) mx = __builtin_fmaxf(mx, s[t][e]);
-      if (__builtin_amdgcn_ballot_w64(mx * kScaleLog2 > mref + kLazy)) {
-        mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = mx * kScaleLog2;
-        const float nref = mnew > mref + kLazy ? mnew : mref;
-        const float alpha = __builtin_amdgcn_exp2f(mref - nref);  // 0 on the first block
-        l *= alpha;
-#pragma unroll
-        for (int dd = 0; dd < 2; ++dd)
-#pragma unroll
-          for (int e = 0; e < 16; ++e) o[dd][e] *= alpha;
-        mref = nref;
-      }
-      const float nm = -mref;
+      prep((kb0 + j) * 64, s);
       // four groups of 8 scores (t, a): their exponentials and P, the two
       // P V products of the group, and two of the next block's S products
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int t = g >> 1, a = g & 1;
-        f16x8 p;
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          p[e] = (f16)__builtin_amdgcn_exp2f(__builtin_fmaf(s[t][8 * a + e], kScaleLog2, nm));
-        // the row sum adds the rounded weights, so out is a weighted mean of V
-#pragma unroll
-        for (int e = 0; e < 8; e += 2)
-          l = __builtin_amdgcn_fdot2((f16x2){p[e], p[e + 1]}, ones, l, false);
+        const f16x8 p = exps(s, g);
         o[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[0][t][a], p, o[0], 0, 0, 0);
         o[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf[1][t][a], p, o[1], 0, 0, 0);
         sn[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[t][2 * a], qh[2 * a],
@@ -300,15 +390,20 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
   }
   if (j < iters) step(j, stage, s, s2);
 
+  }
+
   // each lane summed the weights of its own 32 keys per block; the two lane
   // halves share the reference max, so their sums add
   l += __shfl_xor(l, 32);
 
-  if constexpr (KS == 2) {
-    // the second key group hands (m', sum, O) to the first through LDS (the
-    // ring is free: every wave passed the loop's last barrier)
-    float *xch = reinterpret_cast<float *>(smem) + wq * 34 * 64;
-    if (grp == 1) {
+  if constexpr (KS > 1) {
+    // key groups 1 .. KS-1 hand (m', sum, O) to group 0 through LDS (the
+    // ring is free: every wave passed the loop's last barrier); a group
+    // without blocks hands m' = -inf, sum 0, O 0, which weigh nothing
+    float *base = reinterpret_cast<float *>(smem) + wq * 34 * 64;
+    constexpr int kSlot = 4 * 34 * 64;  // floats per key group
+    if (grp > 0) {
+      float *xch = base + (grp - 1) * kSlot;
       xch[lane] = mref;
       xch[64 + lane] = l;
 #pragma unroll
@@ -317,15 +412,26 @@ __global__ __launch_bounds__(256 * KS) void flash_enc_kernel(
         for (int e = 0; e < 16; ++e) xch[(2 + 16 * dd + e) * 64 + lane] = o[dd][e];
     }
     __syncthreads();
-    if (grp == 1) return;
-    const float mb = xch[lane], lb = xch[64 + lane];
-    const float m = __builtin_fmaxf(mref, mb);
-    const float fa = __builtin_amdgcn_exp2f(mref - m), fb = __builtin_amdgcn_exp2f(mb - m);
-    l = l * fa + lb * fb;
+    if (grp > 0) return;
+    float m = mref;
+#pragma unroll
+    for (int g = 1; g < KS; ++g) m = __builtin_fmaxf(m, base[(g - 1) * kSlot + lane]);
+    const float fa = __builtin_amdgcn_exp2f(mref - m);
+    l *= fa;
 #pragma unroll
     for (int dd = 0; dd < 2; ++dd)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) o[dd][e] = o[dd][e] * fa + xch[(2 + 16 * dd + e) * 64 + lane] * fb;
+      for (int e = 0; e < 16; ++e) o[dd][e] *= fa;
+#pragma unroll
+    for (int g = 1; g < KS; ++g) {
+      const float *xch = base + (g - 1) * kSlot;
+      const float fb = __builtin_amdgcn_exp2f(xch[lane] - m);
+      l += xch[64 + lane] * fb;
+#pragma unroll
+      for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[dd][e] += xch[(2 + 16 * dd + e) * 64 + lane] * fb;
+    }
   }
 
   // out row q0 + r, d = 32dd + 8g + 4h + i from o[dd][4g + i]
@@ -349,11 +455,23 @@ bool overlaps(const void *a, size_t an, const void *b, size_t bn) {
   return x < y + bn && y < x + an;
 }
 
-// Key groups per workgroup: two (two waves per SIMD) while the workgroups do
-// not fill the compute units twice over.
-int key_groups(uint32_t items) {
-  if (const char *e = getenv("MADI_FLASH_KSPLIT")) return atoi(e) == 1 ? 1 : 2;
-  return items < 2u * (uint32_t)cu_count() ? 2 : 1;
+// Key groups per workgroup (waves per SIMD): four, with the plain schedule
+// (measured at 1500 x 20 heads: one group 30.6 us, two pipelined 22.9, three
+// 21.3, four 20.5; four also leads at 40 heads and at 3000 frames);
+// MADI_FLASH_KSPLIT = 1 .. 4 picks another count.
+int key_groups() {
+  if (const char *e = getenv("MADI_FLASH_KSPLIT")) {
+    const int ks = atoi(e);
+    if (ks >= 1 && ks <= 4) return ks;
+  }
+  return 4;
+}
+
+template <int KS, bool PIPE>
+void launch_flash(void *out, const void *q, const void *k, const void *v, uint32_t seq, uint32_t nh,
+                  uint32_t qtiles) {
+  flash_enc_kernel<KS, PIPE><<<nh * qtiles, 256 * KS, 0, stream()>>>(
+      (f16 *)out, (const f16 *)q, (const f16 *)k, (const f16 *)v, seq, nh, qtiles);
 }
 
 }  // namespace
@@ -376,12 +494,11 @@ extern "C" int madi_flash_enc_f16(void *out, const void *q, const void *k, const
     if (int rc = deferred_before_read(in, bytes)) return rc;
   if (int rc = deferred_before_write(out, bytes)) return rc;
   const uint32_t qtiles = (seq_len + kQRows - 1) / kQRows;
-  const uint32_t items = nh * qtiles;
-  if (key_groups(items) == 2)
-    flash_enc_kernel<2><<<items, 512, 0, stream()>>>((f16 *)out, (const f16 *)q, (const f16 *)k,
-                                                     (const f16 *)v, seq_len, nh, qtiles);
-  else
-    flash_enc_kernel<1><<<items, 256, 0, stream()>>>((f16 *)out, (const f16 *)q, (const f16 *)k,
-                                                     (const f16 *)v, seq_len, nh, qtiles);
+  switch (key_groups()) {
+  case 1: launch_flash<1, true>(out, q, k, v, seq_len, nh, qtiles); break;
+  case 2: launch_flash<2, true>(out, q, k, v, seq_len, nh, qtiles); break;
+  case 3: launch_flash<3, false>(out, q, k, v, seq_len, nh, qtiles); break;
+  default: launch_flash<4, false>(out, q, k, v, seq_len, nh, qtiles); break;
+  }
   return check_launch("madi_flash_enc_f16");
 }

@@ -5,8 +5,9 @@ float64 softmax attention, through the C ABI.
 Bars: every element within the bound the f16 rounding of P allows around the
 exact attention (tests/attn_check.py; the kernel's error has the same sources
 as the oracle's), within twice that bound of the oracle, and a normwise
-relative difference from the oracle under 1e-3.  Both kernel variants (one key
-group per workgroup, and two groups splitting the key range) run every case.
+relative difference from the oracle under 1e-3.  Every kernel variant (one
+to four key groups per workgroup splitting the key range; one and two with the
+pipelined schedule, three and four with the plain one) runs every case.
 """
 import os
 import sys
@@ -36,7 +37,7 @@ def q8():
     return q8
 
 
-@pytest.fixture(params=[1, 2], ids=["one_group", "two_groups"])
+@pytest.fixture(params=[1, 2, 3, 4], ids=["one_group", "two_groups", "three_groups", "four_groups"])
 def ksplit(request):
     old = os.environ.get("MADI_FLASH_KSPLIT")
     os.environ["MADI_FLASH_KSPLIT"] = str(request.param)

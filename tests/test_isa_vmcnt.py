@@ -72,11 +72,12 @@ def attn_asm(tmp_path_factory):
 
 
 def test_every_attention_instance_is_race_free(attn_asm):
-    """The encoder attention kernel (one and two key groups): the Q fragments
-    loaded into registers are not touched before their wait, on any of the
-    prologue's paths, and the block loop adds no register loads."""
+    """The encoder attention kernel (one to four key groups, pipelined and
+    plain schedules): the Q fragments loaded into registers are not touched
+    before their wait, on any of the prologue's paths, and the block loop adds
+    no register loads."""
     names = [n for n in attn_asm if "flash_enc_kernel" in n]
-    assert len(names) == 2, names
+    assert len(names) == 4, names
     bad = {n: hazards(attn_asm[n])[:3] for n in names}
     bad = {n: b for n, b in bad.items() if b}
     assert not bad, bad
