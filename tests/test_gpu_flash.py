@@ -43,7 +43,7 @@ def ksplit(request):
     os.environ["MADI_FLASH_KSPLIT"] = str(request.param)
     yield request.param
     if old is None:
-        del os.environ["MADI_FLASH_KSPLIT"]
+        os.environ.pop("MADI_FLASH_KSPLIT", None)
     else:
         os.environ["MADI_FLASH_KSPLIT"] = old
 
