@@ -391,7 +391,288 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT, F32> &p, uint32_t c, 
   }
 }
 
-template <int MT, int EPI, bool PADDED, bool F32 = false>
+// The bias operands of panel (2 * wave + t), 16 bytes per (t, g), loaded from
+// inline asm so the compiler inserts no wait for them: its count would also
+// cover the asm loads issued before or after them (weights still in flight,
+// the persistent loop's next prologue), so the kernels wait with their own.
+__device__ inline void load_bias(f32x4 (&b4)[2][4], const float *bias, uint32_t np, uint32_t p0,
+                                 uint32_t wave, uint32_t h) {
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    uint32_t pb = p0 + 2 * wave + t;
+    pb = pb < np ? pb : np - 1;
+    const desc_t d = make_desc(bias + pb * kPanelRows, kPanelRows * 4);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32x4 v;
+      asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen"
+                   : "=v"(v) : "v"((g * 8 + h * 4) * 4), "s"(d), "s"(sgpr(0u)));
+      b4[t][g] = __builtin_bit_cast(f32x4, v);
+    }
+  }
+#pragma clang diagnostic pop
+}
+
+template <int N>
+__device__ inline void wait_bias(f32x4 (&b4)[2][4]) {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%[n])"
+               : "+v"(b4[0][0]), "+v"(b4[0][1]), "+v"(b4[0][2]), "+v"(b4[0][3]), "+v"(b4[1][0]),
+                 "+v"(b4[1][1]), "+v"(b4[1][2]), "+v"(b4[1][3])
+               : [n] "n"(N));
+}
+
+// LDS accesses of this wave done, then meet the other waves (the C staging
+// handoff of the m-tile-major tail; vector-memory stores stay in flight).
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// ---- m-tile-major tail (unpadded chunk count, one K split, f16 result, two
+// or more m-tiles).  The last four chunks do not run chunk by chunk: m-tile 0
+// runs its MFMAs over all four chunks first (the four chunks' weights
+// dequantised along the way and kept in registers, 32 fragments), then m-tile
+// 1 while m-tile 0 leaves -- its bias, GELU and conversion, LDS transpose and
+// C stores interleaved with m-tile 1's MFMAs -- and so on: only the last
+// m-tile's epilogue follows the last MFMA, and the other m-tiles' stores
+// (bounded by the HBM write rate, since every workgroup writes at once)
+// overlap matrix work.  Every output accumulates in the chunk loop's order
+// (chunk by chunk, k-step by k-step), so the result is bit-identical to it.
+//
+// Entry state (the loop's last trip ended with chunk c-1, c = nchunks - 4,
+// c % 4 == 0): w holds chunk c's step 0-2 fragments, r0 chunk c's weights
+// (landed), r1..r3 the weights of chunks c+1..c+3 and the A stages of chunks
+// c+2 and c+3 are in flight (chunk j's loads, LA DMAs then LW weight loads,
+// were issued in chunk j-4), the stages of chunks c and c+1 are published,
+// af holds every m-tile's step-0 fragment of chunk c.  The ring stages of
+// chunks c-4 .. c-1 (four consecutive stages) are free: no DMA targets them
+// and every read of them completed before the last barrier.  They hold the C
+// staging, one m-tile (32 rows) per buffer.
+template <int MT>
+struct Tail {
+  using G = Geometry<MT>;
+  static constexpr int kCBuf = 32 * kCStride;
+  static constexpr int kBufs = 4 * G::kStage >= 2 * kCBuf ? 2 : 1;
+  static_assert(4 * G::kStage >= kCBuf, "one m-tile of C fits the free ring stages");
+};
+
+// One MFMA, then V vector-ALU ops (its shadow: one wave issues while its
+// MFMA runs, so the two pipes overlap only when their instructions alternate).
+template <int V>
+__device__ inline void mfma_then_valu() {
+  __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
+  if constexpr (V > 0) __builtin_amdgcn_sched_group_barrier(kSchedVALU, V, 0);
+}
+__device__ inline void mfma_then_about(int v) {
+  if (v <= 0) mfma_then_valu<0>();
+  else if (v <= 4) mfma_then_valu<4>();
+  else if (v <= 6) mfma_then_valu<6>();
+  else if (v <= 8) mfma_then_valu<8>();
+  else if (v <= 12) mfma_then_valu<12>();
+  else if (v <= 16) mfma_then_valu<16>();
+  else if (v <= 32) mfma_then_valu<32>();
+  else mfma_then_valu<64>();
+}
+// nm (2 or 4) MFMAs of a tail k-step, each followed by about v VALU ops
+__device__ inline void schedule_tail_step(int nm, int v) {
+  mfma_then_about(v);
+  mfma_then_about(v);
+  if (nm > 2) {
+    mfma_then_about(v);
+    mfma_then_about(v);
+  }
+}
+
+template <int MT, int EPI>
+__device__ inline void tail(uint8_t *smem, uint32_t c, uint32_t h, uint32_t r, uint32_t wave,
+                            f32x16 (&acc)[2][MT], const f16x8 (&w)[2][4], const f16x8 (&af)[MT],
+                            RawW &r0, RawW &r1, RawW &r2, RawW &r3, f16 *__restrict__ Cout,
+                            const float *__restrict__ bias, uint32_t M, uint32_t N, uint32_t m0,
+                            uint32_t p0, uint32_t np) {
+  using G = Geometry<MT>;
+  using TG = Tail<MT>;
+  constexpr int NB = EPI != MADI_EPI_NONE ? 8 : 0;  // bias loads per lane
+  const uint8_t *st[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) st[j] = smem + ((c + j) & (NA - 1)) * G::kStage;
+  uint8_t *stg = smem + ((c + 4) & (NA - 1)) * G::kStage;
+  uint32_t phys[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) phys[s] = ((h * 4 + s) ^ a_swz(r)) * 16;
+
+  // chunk c+1's weights: only chunks c+2 and c+3's loads may be outstanding
+  wait_weights<2 * G::kPerChunk>(r1);
+  f32x4 b4[2][4];
+  if constexpr (NB) load_bias(b4, bias, np, p0, wave, h);
+
+  f16x8 W[4][2][4];  // [chunk c + j][panel][k-step]
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int s = 0; s < 3; ++s) W[0][t][s] = w[t][s];
+
+  // C: rows past M fall outside the resource; columns past N get an offset
+  // past its end (no branch around the stores)
+  const uint32_t rows = M - m0 < 32 * MT ? M - m0 : 32 * MT;
+  const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+      Cout + (size_t)m0 * N, 0, (int)(rows * N * 2), 0x00020000);
+  const uint32_t n = p0 * kPanelRows + r * 8;
+  const uint32_t col_ok = n < N ? 0u : 0x80000000u;
+
+  // the conversion of m-tile q's register group (t, g): bias, GELU, f16, LDS
+  auto epi_group = [&](int q, int t, int g) {
+    uint8_t *Ct = stg + (q % TG::kBufs) * TG::kCBuf;
+    const uint32_t nl = (2 * wave + t) * kPanelRows;
+    float v[4] = {acc[t][q][g * 4 + 0], acc[t][q][g * 4 + 1], acc[t][q][g * 4 + 2],
+                  acc[t][q][g * 4 + 3]};
+    if constexpr (EPI != MADI_EPI_NONE) {
+      v[0] += b4[t][g].x;
+      v[1] += b4[t][g].y;
+      v[2] += b4[t][g].z;
+      v[3] += b4[t][g].w;
+      if constexpr (EPI == MADI_EPI_BIAS_GELU) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = gelu_erf_fast(v[e]);
+      }
+    }
+    const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
+    *reinterpret_cast<f16x4 *>(Ct + r * kCStride + (nl + g * 8 + h * 4) * 2) = o;
+  };
+  // staged rows of m-tile q: lane (h, r) holds 16 bytes of row 2j + h of the
+  // wave's eight, at column 8r
+  u32x4 cv[4];
+  auto epi_read = [&](int q) {
+    const uint8_t *Ct = stg + (q % TG::kBufs) * TG::kCBuf;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      cv[j] = *reinterpret_cast<const u32x4 *>(Ct + (wave * 8 + 2 * j + h) * kCStride + r * 16);
+  };
+  auto epi_store = [&](int q, int j) {
+    const uint32_t row = q * 32 + wave * 8 + 2 * j + h;
+    // 24-bit product (rows < 2^7, N < 2^24): a 32-bit multiply-add, which
+    // the compiler would otherwise form with a 64-bit addend whose unused
+    // high half is an arbitrary live register
+    __builtin_amdgcn_raw_buffer_store_b128(cv[j], cr, ((__umul24(row, N) + n) * 2) | col_ok, 0,
+                                           kSc1);
+  };
+
+  // Passes: pass 0 runs m-tiles [0, P0) (two where there are three or more,
+  // so that sixteen MFMAs per slot cover the dequantisation of the next
+  // chunk), every later pass one m-tile.  Pass p >= 1 also retires the
+  // m-tiles pass p-1 finished: one m-tile is converted over slots 0-1 (a
+  // register group per k-step) and stored in slot 2; two are converted in
+  // slots 0 and 1 (two groups per k-step) and stored in slots 1 and 2.  A
+  // store slot first meets the other waves (the m-tile is staged).
+  constexpr int P0 = MT >= 3 ? 2 : 1;
+  constexpr int NP = MT - P0 + 1;
+  static_assert(TG::kBufs == 2 || MT == 2, "a staging buffer is rewritten only after a barrier");
+  auto first = [](int pp) { return pp == 0 ? 0 : P0 + pp - 1; };
+  auto count = [](int pp) { return pp == 0 ? P0 : 1; };
+
+  // A fragments of slot (p, j) = the pass's m-tiles, chunk c + j, read one slot ahead
+  f16x8 fa[2][P0][4];
+  auto read_frags = [&](int pp, int j, f16x8 (&dst)[P0][4]) {
+#pragma unroll
+    for (int mi = 0; mi < P0; ++mi) {
+      if (mi < count(pp)) {
+        const int i = first(pp) + mi;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          dst[mi][s] = j == 0 && s == 0
+                           ? af[i]
+                           : *reinterpret_cast<const f16x8 *>(st[j] + (i * 32 + r) * 128 + phys[s]);
+      }
+    }
+  };
+  read_frags(0, 0, fa[0]);
+
+#pragma unroll
+  for (int pp = 0; pp < NP; ++pp) {
+    const int R = pp == 0 ? 0 : count(pp - 1), q0 = pp == 0 ? 0 : first(pp - 1);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int cur = (pp * 4 + j) & 1;
+      if (pp == 0 && j == 1) {
+        // chunk c+2's A stage and weights (chunk c+3's loads and the bias may be outstanding)
+        wait_then_barrier<G::kPerChunk + NB>();
+        wait_weights<G::kPerChunk + NB>(r2);
+      }
+      if (pp == 0 && j == 2) {
+        wait_then_barrier<NB>();  // chunk c+3's A stage and weights
+        wait_weights<NB>(r3);
+      }
+      if constexpr (NB) {
+        if (pp == 1 && j == 0) wait_bias<0>(b4);
+      }
+      // the m-tile this slot stores, if any
+      const int sq = R == 1 ? (j == 2 ? q0 : -1) : R == 2 ? (j == 1 ? q0 : j == 2 ? q0 + 1 : -1) : -1;
+      if (sq >= 0) lds_barrier();  // m-tile sq is staged
+      if (pp * 4 + j + 1 < NP * 4) {
+        const int np_ = (pp * 4 + j + 1) / 4, nj = (pp * 4 + j + 1) % 4;
+        read_frags(np_, nj, fa[cur ^ 1]);
+      }
+      if (sq >= 0) epi_read(sq);
+      __builtin_amdgcn_sched_barrier(0);
+      // each k-step: the pass's MFMAs, then a share of the slot's other work
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+#pragma unroll
+        for (int mi = 0; mi < P0; ++mi) {
+          if (mi < count(pp)) {
+            const int i = first(pp) + mi;
+            acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(W[j][0][s], fa[cur][mi][s], acc[0][i], 0, 0, 0);
+            acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(W[j][1][s], fa[cur][mi][s], acc[1][i], 0, 0, 0);
+          }
+        }
+        if (pp == 0) {
+          // the next chunk's fragments (t, u) = (s >> 1, 2 (s & 1) ..), and
+          // this chunk's step-3 fragments at step 0
+          if (j == 0 && s == 0) {
+            W[0][0][3] = dequant_frag(r0, 0, 3);
+            W[0][1][3] = dequant_frag(r0, 1, 3);
+          }
+          if (j < 3) {
+            const RawW &src = j == 0 ? r1 : j == 1 ? r2 : r3;
+            const int t = s >> 1, u = 2 * (s & 1);
+            W[j + 1][t][u] = dequant_frag(src, t, u);
+            W[j + 1][t][u + 1] = dequant_frag(src, t, u + 1);
+          }
+        }
+        if (R == 1 && j < 2) {
+          const int g8 = 4 * j + s;
+          epi_group(q0, g8 >> 2, g8 & 3);
+        }
+        if (R == 2 && j < 2) {
+          epi_group(q0 + j, s >> 1, 2 * (s & 1));
+          epi_group(q0 + j, s >> 1, 2 * (s & 1) + 1);
+        }
+        if (sq >= 0) epi_store(sq, s);
+        // VALU ops of the step: 12 per dequantised fragment; per converted
+        // register group 6 (accumulator reads, conversions), 4 more with a
+        // bias, ~44 more with GELU; 2 for a store's address
+        constexpr int kGroupOps = 6 + (EPI != MADI_EPI_NONE ? 4 : 0) + (EPI == MADI_EPI_BIAS_GELU ? 44 : 0);
+        const int nm = 2 * count(pp);
+        const int ops = (pp == 0 ? (j < 3 ? 24 : 0) + (j == 0 && s == 0 ? 24 : 0) : 0) +
+                        (R == 1 && j < 2 ? kGroupOps : 0) + (R == 2 && j < 2 ? 2 * kGroupOps : 0) +
+                        (sq >= 0 ? 2 : 0);
+        schedule_tail_step(nm, (ops + nm - 1) / nm);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  if (TG::kBufs == 1) lds_barrier();  // m-tile MT-2's rows are read
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) epi_group(MT - 1, t, g);
+  lds_barrier();
+  epi_read(MT - 1);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) epi_store(MT - 1, j);
+}
+
+
+template <int MT, int EPI, bool PADDED, bool F32 = false, bool TAIL = false>
 __global__ __launch_bounds__(256) void q8_gemm_kernel(
     const void *__restrict__ A, const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
     uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m, uint32_t tiles_n, uint32_t group_m,
@@ -399,6 +680,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     float *__restrict__ ws, uint32_t *__restrict__ cnt) {
   using G = Geometry<MT, F32>;
   static_assert(!F32 || EPI == MADI_EPI_NONE, "f32 output has no bias epilogue");
+  static_assert(!TAIL || (!PADDED && !F32 && MT >= 2), "the m-tile-major tail's shapes");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G::kLds];
   __shared__ uint32_t arrived;
 
@@ -521,10 +803,17 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
       chunk<MT, F32, kLive, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
       c += 4;
     } while (c + 2 * WD <= nchunks);
-    chunk<MT, F32, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-    chunk<MT, F32, kLast1, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-    chunk<MT, F32, kLast2, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-    chunk<MT, F32, kLast3, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+    if constexpr (TAIL) {
+      // one K split (the host checks): the tile's epilogue is the tail's
+      tail<MT, EPI>(smem, c, h, r, wave, acc, w, af, r0, r1, r2, r3, static_cast<f16 *>(Cout),
+                    bias, M, N, m0, p0, np);
+      return;
+    } else {
+      chunk<MT, F32, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
+      chunk<MT, F32, kLast1, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
+      chunk<MT, F32, kLast2, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
+      chunk<MT, F32, kLast3, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+    }
   }
 
   drain(r0, r1, r2, r3);
@@ -745,38 +1034,6 @@ struct Persist {
   static constexpr int kCBuf = 32 * kCStride;  // one m-tile of the C tile
   static_assert(4 * kStage + 2 * kCBuf <= Geometry<MT>::kRing, "C staging fits stages 4-7");
 };
-
-// The bias operands of panel (2 * wave + t), 16 bytes per (t, g), loaded from
-// inline asm so the compiler inserts no wait for them (its count would also
-// cover the next tile's prologue loads issued before them).
-__device__ inline void load_bias(f32x4 (&b4)[2][4], const float *bias, uint32_t np, uint32_t p0,
-                                 uint32_t wave, uint32_t h) {
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    uint32_t pb = p0 + 2 * wave + t;
-    pb = pb < np ? pb : np - 1;
-    const desc_t d = make_desc(bias + pb * kPanelRows, kPanelRows * 4);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32x4 v;
-      asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen"
-                   : "=v"(v) : "v"((g * 8 + h * 4) * 4), "s"(d), "s"(sgpr(0u)));
-      b4[t][g] = __builtin_bit_cast(f32x4, v);
-    }
-  }
-#pragma clang diagnostic pop
-}
-
-template <int N>
-__device__ inline void wait_bias(f32x4 (&b4)[2][4]) {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%[n])"
-               : "+v"(b4[0][0]), "+v"(b4[0][1]), "+v"(b4[0][2]), "+v"(b4[0][3]), "+v"(b4[1][0]),
-                 "+v"(b4[1][1]), "+v"(b4[1][2]), "+v"(b4[1][3])
-               : [n] "n"(N));
-}
 
 template <int EPI>
 __global__ __launch_bounds__(256) void q8_gemm_persist_kernel(
@@ -1385,6 +1642,13 @@ int resolve_scratch(uint8_t **out) {
   return MADI_OK;
 }
 
+// The m-tile-major tail serves unpadded, unsplit f16 launches of two or more
+// m-tiles (MADI_GEMM_TAIL=0 selects the chunk-by-chunk last trip instead).
+bool use_tail(uint32_t splits) {
+  const char *e = getenv("MADI_GEMM_TAIL");
+  return splits == 1 && !(e && e[0] == '0');
+}
+
 // Where a launch keeps its split-K partials and counters.
 enum Scratch { kWorkspace = 0, kStatic = 1 };
 
@@ -1427,7 +1691,16 @@ int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const 
     hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, true, F32>), dim3(T, splits), dim3(kWaves * 64),
                        0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
                        bias, ws, cnt);
-  else
+  else if constexpr (!F32 && MT >= 2) {
+    if (use_tail(splits))
+      hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false, false, true>), dim3(T, splits),
+                         dim3(kWaves * 64), 0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n,
+                         group_m, cper, crem, C, bias, ws, cnt);
+    else
+      hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false, false>), dim3(T, splits),
+                         dim3(kWaves * 64), 0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n,
+                         group_m, cper, crem, C, bias, ws, cnt);
+  } else
     hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false, F32>), dim3(T, splits), dim3(kWaves * 64),
                        0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
                        bias, ws, cnt);

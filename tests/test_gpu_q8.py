@@ -336,6 +336,46 @@ def test_gemm_encoder_epilogues_full_m(q, name, n, k, gelu):
         assert np.all(np.isfinite(c))
 
 
+@pytest.mark.parametrize("m,n,k,epi", [
+    (33, 320, 512, O.EPI_NONE),         # 64-row tiles, one staging buffer, columns past N
+    (60, 320, 768, O.EPI_BIAS_GELU),
+    (700, 8000, 768, O.EPI_BIAS),       # 96-row tiles, columns past N, M tail
+    (700, 8000, 1024, O.EPI_NONE),
+    (800, 8000, 512, O.EPI_BIAS_GELU),  # 128-row tiles: one full trip, then the tail
+    (1500, 5120, 1280, O.EPI_BIAS_GELU),  # fc1 of the encoder
+    (1500, 2560, 1280, O.EPI_BIAS),     # cross K|V: 64-row tiles
+])
+def test_gemm_tail_matches_chunk_loop(q, m, n, k, epi):
+    """The m-tile-major tail (the last four chunks one m-tile at a time, each
+    m-tile's epilogue under the next one's MFMAs) against the chunk-by-chunk
+    last trip (MADI_GEMM_TAIL=0): the accumulation order is the same, so the
+    results agree bit for bit; the oracle checks a row sample of both."""
+    import os
+    say(f"gemm tail vs chunk loop m={m} n={n} k={k} epi={epi}")
+    a, qs, sc = synth.gemm_case(m * 3 + n + k, m, n, k)
+    bias = np.random.default_rng(k).standard_normal(n).astype(np.float32)
+    b = None if epi == O.EPI_NONE else bias
+    gelu = epi == O.EPI_BIAS_GELU
+    old = os.environ.pop("MADI_GEMM_TAIL", None)
+    try:
+        c_tail = _gemm(q, a, qs, sc, bias=b, gelu=gelu)
+        os.environ["MADI_GEMM_TAIL"] = "0"
+        c_loop = _gemm(q, a, qs, sc, bias=b, gelu=gelu)
+    finally:
+        os.environ.pop("MADI_GEMM_TAIL", None)
+        if old is not None:
+            os.environ["MADI_GEMM_TAIL"] = old
+    assert np.array_equal(c_tail.view(np.uint16), c_loop.view(np.uint16))
+    rows = tile_rows(m)
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, bias=b, epilogue=epi, threads=16)
+    assert normwise(c_tail[rows], ref) <= TOL
+    if b is None:
+        assert tight_ok(c_tail[rows], a[rows], qs, sc)
+    else:
+        assert tight_epi_ok(c_tail[rows], a[rows], qs, sc, bias, gelu)
+    assert np.all(np.isfinite(c_tail))
+
+
 @pytest.mark.parametrize("name,n,k", [("fc1", 5120, 1280), ("fc2", 1280, 5120)])
 def test_gemm_long_audio_full_m(q, name, n, k):
     """16 stacked windows, M = 24000: 128-row tiles, 188 x 20 (fc1) and 188 x 5
