@@ -493,6 +493,42 @@ def test_gemv_zero_blocks_are_exact(q, x_f16):
     assert normwise(got, ref) <= 1e-5
 
 
+@pytest.mark.parametrize("case", ["full_mantissa", "huge", "tiny", "mixed_in_block", "zero_blocks"])
+def test_gemv_f32_activations(q, case):
+    """f32 activations with full 24-bit mantissas and wide ranges: the kernel
+    splits each 32-element block, scaled by a power of two, into f16 high and
+    low halves, so every product keeps ~22 bits.  Bar per row: the float64
+    sum within (K 2^-24 + 2^-21) sum_k |x_k q_k s_k| (f32 accumulation plus
+    the split), far below what a lost scale factor or a dropped half makes."""
+    n, k = 256, 1280
+    rng = np.random.default_rng(7 * len(case) + ord(case[0]))
+    qs, sc = synth.q8_weight(rng, n, k)
+    x = rng.standard_normal(k).astype(np.float32)
+    if case == "huge":
+        x *= np.float32(3e30)
+    elif case == "tiny":
+        x *= np.float32(2e-30)
+    elif case == "mixed_in_block":
+        x *= (10.0 ** rng.uniform(-6, 6, k)).astype(np.float32)
+    elif case == "zero_blocks":
+        x[64:160] = 0.0
+        x[1000:1024] = 0.0
+    say(f"gemv f32 x {case}")
+    w = q.upload_q8(qs, sc)
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    q.kGemvQ8(out, dev(x), w, n, k)
+    q.sync()
+    got = out.cpu().numpy().astype(np.float64)
+    w64 = (qs.astype(np.float64) * np.repeat(sc.astype(np.float64), 32, axis=1))  # [N][K]
+    exact = w64 @ x.astype(np.float64)
+    mag = np.abs(w64) @ np.abs(x.astype(np.float64))
+    bound = (k * 2.0**-24 + 2.0**-21) * mag
+    assert np.all(np.isfinite(got))
+    assert np.all(np.abs(got - exact) <= bound), np.max(np.abs(got - exact) / np.maximum(bound, 1e-300))
+    ref = O.q8_gemv(x, qs, sc, threads=4)
+    assert normwise(got, ref) <= 1e-5
+
+
 def test_logit_gemv_vocab(q):
     n, k = 51866, 1280
     x16, qs, sc = synth.gemv_case(0, n, k)
