@@ -81,31 +81,33 @@ constexpr int kSplitTile = 2;       // m-tiles per tile where 128-row tiles woul
 // F32: the activations arrive as f32 (rounded to f16 on their way from LDS to
 // the MFMA) and the result leaves as f32 -- the batched projection's operand
 // types (the engine's f32 rows, staged to f16 for the GEMM).
-template <int MT, bool F32 = false>
+template <int MT, bool F32 = false, int PW = 2>
 struct Geometry {
   static constexpr int kRowBytes = F32 ? 256 : 128;  // one A row of a 64-wide chunk
   static constexpr int kStage = MT * 32 * kRowBytes;  // one A stage (32*MT rows)
   static constexpr int kRing = NA * kStage;
-  static constexpr int kCPitch = F32 ? kPanelsPerTile * kPanelRows * 4 + 16 : kCStride;
+  static constexpr int kTilePanels = 4 * PW;  // panels (32 columns each) per tile
+  static constexpr int kCPitch =
+      F32 ? kPanelsPerTile * kPanelRows * 4 + 16 : kTilePanels * kPanelRows * 2 + 16;
   static constexpr int kCTile = 32 * MT * kCPitch;
   static constexpr int kLds = kRing > kCTile ? kRing : kCTile;
   // vector-memory instructions per wave per chunk, spread over the four
   // k-steps so the texture pipe never sees a burst: step 0 the first half of
   // the A DMA (LA DMAs of 1 KiB: 8 f16 rows or 4 f32 rows each), step 1 its
   // second half and weight unit (0,0), step 2 units (0,1) and (1,0), step 3
-  // unit (1,1) and the two scales
+  // unit (1,1) and the scales (one panel: units (0,0), (0,1), the scale)
   static constexpr int LA = F32 ? 2 * MT : MT;
   static constexpr int LA0 = LA >= 2 ? (LA + 1) / 2 : 0;  // DMAs issued in step 0
-  static constexpr int LW = 6;
+  static constexpr int LW = 3 * PW;
   static constexpr int kPerChunk = LA + LW;
-  static constexpr int kBeforeStep3 = LA + 3;  // issued in steps 0..2
+  static constexpr int kBeforeStep3 = LA + (PW == 2 ? 3 : 2);  // issued in steps 0..2
   // at the start of chunk c: the weights of chunk c+1 (the last loads of
   // chunk c+1-WD) have landed once only the loads of the WD-2 chunks after
   // them are outstanding
   static constexpr int kVmRaw = (WD - 2) * kPerChunk;
   // before step 3 of an odd chunk c, whose barrier publishes the A stages of
   // chunks c+1 and c+2: chunk c+2's stage (issued in steps 0-1 of chunk
-  // c+2-DA, followed by that chunk's 6 weight loads, chunk c-1's loads and
+  // c+2-DA, followed by that chunk's LW weight loads, chunk c-1's loads and
   // chunk c's first three steps) has landed
   static constexpr int kVmA = LW + (DA - 3) * kPerChunk + kBeforeStep3;
   // prologue: virtual chunks -DA..-1 issue the same pattern; chunk 0's weights
@@ -121,21 +123,27 @@ struct Geometry {
 __device__ inline uint32_t a_swz(uint32_t row) { return (row >> 1) & 7; }
 __device__ inline uint32_t a_swz32(uint32_t row) { return row & 15; }
 
-// One chunk's int8 weight units and scales of the wave's two panels
-struct RawW {
-  u32x4 u[2][2];   // [panel t][unit j]: k = 32h + 16j + 0..15 of row r
-  uint32_t s[2];   // fp16 scale bits of block h, row r (low half)
+// One chunk's int8 weight units and scales of the wave's PW panels (two in
+// 256-column tiles, one in 128-column tiles)
+template <int PW = 2>
+struct RawWT {
+  u32x4 u[PW][2];  // [panel t][unit j]: k = 32h + 16j + 0..15 of row r
+  uint32_t s[PW];  // fp16 scale bits of block h, row r (low half)
 };
+using RawW = RawWT<2>;
 
 // Wait until `w`'s loads have landed: at most N later loads outstanding.  The
 // registers are operands, so no use of them can be scheduled before the wait.
-template <int N>
-__device__ inline void wait_weights(RawW &w) {
+template <int N, int PW>
+__device__ inline void wait_weights(RawWT<PW> &w) {
   static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%[n])"
-               : "+v"(w.u[0][0]), "+v"(w.u[0][1]), "+v"(w.u[1][0]), "+v"(w.u[1][1]), "+v"(w.s[0]),
-                 "+v"(w.s[1])
-               : [n] "n"(N));
+  if constexpr (PW == 2)
+    asm volatile("s_waitcnt vmcnt(%[n])"
+                 : "+v"(w.u[0][0]), "+v"(w.u[0][1]), "+v"(w.u[1][0]), "+v"(w.u[1][1]),
+                   "+v"(w.s[0]), "+v"(w.s[1])
+                 : [n] "n"(N));
+  else
+    asm volatile("s_waitcnt vmcnt(%[n])" : "+v"(w.u[0][0]), "+v"(w.u[0][1]), "+v"(w.s[0]) : [n] "n"(N));
 }
 
 // After the K loop: wait for every outstanding load, with the four weight
@@ -143,23 +151,31 @@ __device__ inline void wait_weights(RawW &w) {
 // dead to the compiler once the loop ends, and it would otherwise reuse them
 // (for the epilogue's accumulator reads) while loads into them are still in
 // flight.
-__device__ inline void drain(RawW &a, RawW &b, RawW &c, RawW &d) {
-  asm volatile("s_waitcnt vmcnt(0)"
-               : "+v"(a.u[0][0]), "+v"(a.u[0][1]), "+v"(a.u[1][0]), "+v"(a.u[1][1]), "+v"(a.s[0]),
-                 "+v"(a.s[1]), "+v"(b.u[0][0]), "+v"(b.u[0][1]), "+v"(b.u[1][0]), "+v"(b.u[1][1]),
-                 "+v"(b.s[0]), "+v"(b.s[1])::"memory");
-  asm volatile("s_waitcnt vmcnt(0)"
-               : "+v"(c.u[0][0]), "+v"(c.u[0][1]), "+v"(c.u[1][0]), "+v"(c.u[1][1]), "+v"(c.s[0]),
-                 "+v"(c.s[1]), "+v"(d.u[0][0]), "+v"(d.u[0][1]), "+v"(d.u[1][0]), "+v"(d.u[1][1]),
-                 "+v"(d.s[0]), "+v"(d.s[1])::"memory");
+template <int PW>
+__device__ inline void drain(RawWT<PW> &a, RawWT<PW> &b, RawWT<PW> &c, RawWT<PW> &d) {
+  if constexpr (PW == 2) {
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(a.u[0][0]), "+v"(a.u[0][1]), "+v"(a.u[1][0]), "+v"(a.u[1][1]), "+v"(a.s[0]),
+                   "+v"(a.s[1]), "+v"(b.u[0][0]), "+v"(b.u[0][1]), "+v"(b.u[1][0]), "+v"(b.u[1][1]),
+                   "+v"(b.s[0]), "+v"(b.s[1])::"memory");
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(c.u[0][0]), "+v"(c.u[0][1]), "+v"(c.u[1][0]), "+v"(c.u[1][1]), "+v"(c.s[0]),
+                   "+v"(c.s[1]), "+v"(d.u[0][0]), "+v"(d.u[0][1]), "+v"(d.u[1][0]), "+v"(d.u[1][1]),
+                   "+v"(d.s[0]), "+v"(d.s[1])::"memory");
+  } else {
+    asm volatile("s_waitcnt vmcnt(0)"
+                 : "+v"(a.u[0][0]), "+v"(a.u[0][1]), "+v"(a.s[0]), "+v"(b.u[0][0]), "+v"(b.u[0][1]),
+                   "+v"(b.s[0]), "+v"(c.u[0][0]), "+v"(c.u[0][1]), "+v"(c.s[0]), "+v"(d.u[0][0]),
+                   "+v"(d.u[0][1]), "+v"(d.s[0])::"memory");
+  }
 }
 
 // Per-wave load plan, fixed for the whole K loop.
-template <int MT, bool F32>
+template <int MT, bool F32, int PW = 2>
 struct Plan {
   desc_t wq, ws, wa, zero;  // weights, scales, activations, empty
-  uint32_t w_soff[2];       // byte offset of panel (2*wave + t) in the weights
-  uint32_t s_voff[2];       // per-lane byte offset of this lane's scale, panel t
+  uint32_t w_soff[PW];      // byte offset of panel (PW*wave + t) in the weights
+  uint32_t s_voff[PW];      // per-lane byte offset of this lane's scale, panel t
   uint32_t a_voff[Geometry<MT, F32>::LA];  // per-lane activation offsets of the wave's
                             // DMAs, less each DMA's instruction offset (1024 * DMA)
   uint32_t a_lds;           // the wave's first A row within an A stage
@@ -167,13 +183,13 @@ struct Plan {
 };
 
 // DMA I of the wave's share of one chunk's A stage.
-template <int MT, bool F32, int I>
-__device__ inline void dma_group(desc_t wa, const Plan<MT, F32> &p, uint32_t c, uint32_t m0) {
+template <int MT, bool F32, int I, int PW>
+__device__ inline void dma_group(desc_t wa, const Plan<MT, F32, PW> &p, uint32_t c, uint32_t m0) {
   dma16<I * 1024, I == 0>(wa, p.a_voff[I], c * Geometry<MT, F32>::kRowBytes, m0);
 }
 // DMAs I .. END-1
-template <int MT, bool F32, int I, int END>
-__device__ inline void dma_range(desc_t wa, const Plan<MT, F32> &p, uint32_t c, uint32_t m0) {
+template <int MT, bool F32, int I, int END, int PW>
+__device__ inline void dma_range(desc_t wa, const Plan<MT, F32, PW> &p, uint32_t c, uint32_t m0) {
   if constexpr (I < END) {
     dma_group<MT, F32, I>(wa, p, c, m0);
     dma_range<MT, F32, I + 1, END>(wa, p, c, m0);
@@ -199,9 +215,9 @@ enum Prefetch { kSel = 0, kLive = 1, kLast0 = 2, kLast1 = 3, kLast2 = 4, kLast3 
 // prologue loads are followed by E other vector-memory issues (the previous
 // tile's epilogue) before the K loop: the waits whose targets lie in the
 // prologue (chunks 0-2's weights, chunk 3's A stage) allow E more.
-template <int MT, bool F32, int PF, int E = 0>
+template <int MT, bool F32, int PF, int E = 0, int PW = 2>
 struct Waits {
-  using G = Geometry<MT, F32>;
+  using G = Geometry<MT, F32, PW>;
   static constexpr int raw = PF == kLiveE ? G::kVmRaw + E
                            : PF == kLast1 ? G::kPerChunk
                            : (PF >= kLast2 && PF <= kLast3) ? 0
@@ -215,10 +231,10 @@ struct Waits {
 
 // The vector-memory issues of k-step s for chunk c's A stage (into `slot`) and
 // chunk cw's weights (into `w`).
-template <int MT, bool F32, int PF>
-__device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, uint32_t cw,
-                                   const Plan<MT, F32> &p, uint32_t lane) {
-  using G = Geometry<MT, F32>;
+template <int MT, bool F32, int PF, int PW>
+__device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawWT<PW> &w, uint32_t cw,
+                                   const Plan<MT, F32, PW> &p, uint32_t lane) {
+  using G = Geometry<MT, F32, PW>;
   static_assert(DA == 4 && WD == 4, "the last trip's issue plan assumes four-chunk prefetch");
   if constexpr (PF >= kLast0) return;
   desc_t wa = p.wa, wq = p.wq, ws = p.ws;
@@ -238,12 +254,12 @@ __device__ inline void issue_loads(int s, uint8_t *slot, uint32_t c, RawW &w, ui
   } else if (s == 2) {
     if constexpr (W) {
       vload16<1024>(w.u[0][1], wq, lane * 16, p.w_soff[0] + cw * 2048);
-      vload16(w.u[1][0], wq, lane * 16, p.w_soff[1] + cw * 2048);
+      if constexpr (PW == 2) vload16(w.u[1][0], wq, lane * 16, p.w_soff[1] + cw * 2048);
     }
   } else if constexpr (W) {
-    vload16<1024>(w.u[1][1], wq, lane * 16, p.w_soff[1] + cw * 2048);
+    if constexpr (PW == 2) vload16<1024>(w.u[1][1], wq, lane * 16, p.w_soff[1] + cw * 2048);
     vload2(w.s[0], ws, p.s_voff[0], cw * 128);
-    vload2(w.s[1], ws, p.s_voff[1], cw * 128);
+    if constexpr (PW == 2) vload2(w.s[1], ws, p.s_voff[1], cw * 128);
   }
 }
 
@@ -294,7 +310,8 @@ struct AFrag<true> {
 // pairs go through perm, subtract and multiply stage by stage (four
 // independent chains), so no packed op directly follows the one it depends on
 // (which would cost a wait state).
-__device__ inline f16x8 dequant_frag(const RawW &w, int t, int s) {
+template <int PW>
+__device__ inline f16x8 dequant_frag(const RawWT<PW> &w, int t, int s) {
   const u32x4 u = w.u[t][s >> 1];
   const uint32_t b0 = (s & 1) ? u.z : u.x, b1 = (s & 1) ? u.w : u.y;
   const f16 sc = __builtin_bit_cast(f16, (uint16_t)w.s[t]);
@@ -322,34 +339,35 @@ constexpr int kSchedDSRead = 0x100;
 // Instruction order of one k-step: its LDS reads first (their latency hides
 // under this step's MFMAs), then each MFMA followed by up to three VALU ops
 // (the dequantisation, 24 per step) and a vector-memory issue.
-template <int MT, bool F32 = false>
+template <int MT, bool F32 = false, int PW = 2>
 __device__ inline void schedule_step() {
   if constexpr (F32) __builtin_amdgcn_sched_group_barrier(kSchedVALU, 4 * MT, 0);  // f32 -> f16
   __builtin_amdgcn_sched_group_barrier(kSchedDSRead, F32 ? 2 * MT : MT, 0);
 #pragma unroll
-  for (int i = 0; i < 2 * MT; ++i) {
+  for (int i = 0; i < PW * MT; ++i) {
     __builtin_amdgcn_sched_group_barrier(kSchedMFMA, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(kSchedVALU, 24 / (2 * MT) + 1, 0);
+    __builtin_amdgcn_sched_group_barrier(kSchedVALU, 12 / MT + 1, 0);
     __builtin_amdgcn_sched_group_barrier(kSchedVMEM, 1, 0);
   }
 }
 
-// One chunk c.  On entry w holds chunk c's fragments except w[0][3] and
-// w[1][3] (made at step 0 from `cur`, chunk c's weights), `af` holds chunk c's step-0
+// One chunk c.  On entry w holds chunk c's fragments except each panel's
+// w[t][3] (made at step 0 from `cur`, chunk c's weights), `af` holds chunk c's step-0
 // activation fragments (f32: their raw values, rounded at the step's start),
 // and `nxt` receives chunk c+1's weights (loaded WD-1 chunks ago; waited for
 // here).  `ld` (the same register set as `cur`, free after step 0) receives
 // chunk c+WD's weights.
-template <int MT, bool F32, int PF, bool ODD, int E = 0>
-__device__ inline void chunk(uint8_t *smem, const Plan<MT, F32> &p, uint32_t c, uint32_t lane,
-                             uint32_t h, uint32_t r, f32x16 (&acc)[2][MT], f16x8 (&w)[2][4],
-                             typename AFrag<F32>::T (&af)[MT], const RawW &cur, RawW &nxt,
-                             RawW &ld) {
-  using G = Geometry<MT, F32>;
+template <int MT, bool F32, int PF, bool ODD, int E = 0, int PW = 2>
+__device__ inline void chunk(uint8_t *smem, const Plan<MT, F32, PW> &p, uint32_t c, uint32_t lane,
+                             uint32_t h, uint32_t r, f32x16 (&acc)[PW][MT], f16x8 (&w)[PW][4],
+                             typename AFrag<F32>::T (&af)[MT], const RawWT<PW> &cur,
+                             RawWT<PW> &nxt, RawWT<PW> &ld) {
+  using G = Geometry<MT, F32, PW>;
+  using WT = Waits<MT, F32, PF, E, PW>;
   const uint8_t *At = smem + (c % NA) * G::kStage;
   const uint8_t *An = smem + ((c + 1) % NA) * G::kStage;
   uint8_t *Af = smem + ((c + DA) % NA) * G::kStage;
-  wait_weights<Waits<MT, F32, PF, E>::raw>(nxt);
+  wait_weights<WT::raw>(nxt);
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     // the previous step's fragment reads (issued a whole step ago) have
@@ -357,7 +375,7 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT, F32> &p, uint32_t c, 
     // odd chunks: the A stages of chunks c+1 and c+2 become visible, and the
     // stages of chunks c-1 and c retire (refilled from chunk c+DA-2 on); an
     // even chunk reads chunk c+1's stage, published one chunk earlier
-    if (s == 3 && ODD) wait_then_barrier<Waits<MT, F32, PF, E>::a>();
+    if (s == 3 && ODD) wait_then_barrier<WT::a>();
     __builtin_amdgcn_s_waitcnt(kLgkm0);
     f16x8 a16[MT];
 #pragma unroll
@@ -373,20 +391,19 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT, F32> &p, uint32_t c, 
     else
       load_a_frags<MT>(An, 0, h, r, an);
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
-      acc[0][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[0][s], a16[i], acc[0][i], 0, 0, 0);
-    // each panel's step s-1 fragment was consumed last step, at least 2*MT
-    // MFMAs before its refill here (no read-after-write wait states): its
-    // next value is chunk c's own step-3 fragment at step 0, else chunk c+1's
-    w[0][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 0, (s + 3) & 3);
+    for (int t = 0; t < PW; ++t) {
 #pragma unroll
-    for (int i = 0; i < MT; ++i)
-      acc[1][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[1][s], a16[i], acc[1][i], 0, 0, 0);
-    w[1][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, 1, (s + 3) & 3);
+      for (int i = 0; i < MT; ++i)
+        acc[t][i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(w[t][s], a16[i], acc[t][i], 0, 0, 0);
+      // each panel's step s-1 fragment was consumed last step, at least MT
+      // MFMAs before its refill here (no read-after-write wait states): its
+      // next value is chunk c's own step-3 fragment at step 0, else chunk c+1's
+      w[t][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, t, (s + 3) & 3);
+    }
     issue_loads<MT, F32, PF == kLiveE ? kLive : PF>(s, Af, c + DA, ld, c + WD, p, lane);
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[i] = an[i];
-    schedule_step<MT, F32>();
+    schedule_step<MT, F32, PW>();
     __builtin_amdgcn_sched_barrier(0);
   }
 }
@@ -672,15 +689,16 @@ __device__ inline void tail(uint8_t *smem, uint32_t c, uint32_t h, uint32_t r, u
 }
 
 
-template <int MT, int EPI, bool PADDED, bool F32 = false, bool TAIL = false>
+template <int MT, int EPI, bool PADDED, bool F32 = false, bool TAIL = false, int PW = 2>
 __global__ __launch_bounds__(256) void q8_gemm_kernel(
     const void *__restrict__ A, const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
     uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m, uint32_t tiles_n, uint32_t group_m,
     uint32_t cper, uint32_t crem, void *__restrict__ Cout, const float *__restrict__ bias,
     float *__restrict__ ws, uint32_t *__restrict__ cnt) {
-  using G = Geometry<MT, F32>;
+  using G = Geometry<MT, F32, PW>;
   static_assert(!F32 || EPI == MADI_EPI_NONE, "f32 output has no bias epilogue");
-  static_assert(!TAIL || (!PADDED && !F32 && MT >= 2), "the m-tile-major tail's shapes");
+  static_assert(!TAIL || (!PADDED && !F32 && MT >= 2 && PW == 2), "the m-tile-major tail's shapes");
+  static_assert(PW == 2 || (!PADDED && !F32), "128-column tiles: unpadded f16 launches");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G::kLds];
   __shared__ uint32_t arrived;
 
@@ -709,22 +727,22 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t h = lane >> 5, r = lane & 31;
-  const uint32_t m0 = tm * 32 * MT, p0 = tn * kPanelsPerTile;
+  const uint32_t m0 = tm * 32 * MT, p0 = tn * G::kTilePanels;
   const uint32_t np = N / kPanelRows;
   const uint32_t cb = split * cper + (split < crem ? split : crem);
   const uint32_t nchunks = cper + (split < crem ? 1 : 0);
 
   // ---- load plan.  Panels past N and rows past M are clamped to the last
   // valid one: their bytes are read but their results are never stored.
-  Plan<MT, F32> p;
+  Plan<MT, F32, PW> p;
   p.wq = make_desc(qs, N * K);
   p.ws = make_desc(sc, N * K / 16);
   p.wa = make_desc(A, M * K * (F32 ? 4 : 2));
   p.zero = make_desc(A, 0);
   p.nchunks = nchunks;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    uint32_t pp = p0 + 2 * wave + t;
+  for (int t = 0; t < PW; ++t) {
+    uint32_t pp = p0 + PW * wave + t;
     pp = pp < np ? pp : np - 1;
     p.w_soff[t] = pp * kPanelRows * K + cb * 2048;
     p.s_voff[t] = pp * K * 2 + cb * 128 + lane * 2;  // panel pp's chunk c scales at pp*K + 64c elements
@@ -744,9 +762,9 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   }
   p.a_lds = G::LA * wave * 1024;
 
-  f32x16 acc[2][MT];
+  f32x16 acc[PW][MT];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < PW; ++t)
 #pragma unroll
     for (int i = 0; i < MT; ++i) acc[t][i] = (f32x16){};
 
@@ -755,13 +773,13 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   // hold from the first chunk on.  Virtual chunk j loads A stage j+DA and
   // weights j+WD (stages and weights past the last chunk load zeros); register
   // set k receives chunks k, k+WD, ...
-  RawW r0, r1, r2, r3;
+  RawWT<PW> r0, r1, r2, r3;
   static_assert(WD == 4 && DA == 4, "the loop below rotates four weight register sets");
   static_assert(NA >= DA + 2, "an A stage is refilled only after the barrier that retires it");
 #pragma unroll
   for (int j = -4; j < 0; ++j) {
     uint8_t *slot = smem + (uint32_t)(j + DA) * G::kStage;
-    RawW &rw = j == -4 ? r0 : j == -3 ? r1 : j == -2 ? r2 : r3;
+    RawWT<PW> &rw = j == -4 ? r0 : j == -3 ? r1 : j == -2 ? r2 : r3;
 #pragma unroll
     for (int st = 0; st < 4; ++st)
       issue_loads<MT, F32, kSel>(st, slot, (uint32_t)(j + DA), rw, (uint32_t)(j + WD), p, lane);
@@ -770,12 +788,12 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   // chunk 1's stage without a barrier of its own), then chunk 0's fragments
   wait_then_barrier<G::kVmPrologue>();
   wait_weights<G::kVmPrologue>(r0);
-  f16x8 w[2][4];
+  f16x8 w[PW][4];
   typename AFrag<F32>::T af[MT];
 #pragma unroll
-  for (int s = 0; s < 3; ++s) w[0][s] = dequant_frag(r0, 0, s);
+  for (int t = 0; t < PW; ++t)
 #pragma unroll
-  for (int s = 0; s < 3; ++s) w[1][s] = dequant_frag(r0, 1, s);
+    for (int s = 0; s < 3; ++s) w[t][s] = dequant_frag(r0, t, s);
   load_a_frags<MT>(smem, 0, h, r, af);
 
   // ---- main loop: four chunks per trip (the weight register sets rotate).
@@ -819,9 +837,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   drain(r0, r1, r2, r3);
 
   // ---- epilogue.  Lane (h, r) holds D[n][m] for m = 32i + r and
-  // n = 32(2w + t) + 8g + 4h + e (acc[t][i][4g + e]).  Every wave must finish
+  // n = 32(PW w + t) + 8g + 4h + e (acc[t][i][4g + e]).  Every wave must finish
   // reading the ring before it becomes the C tile.
   wait_then_barrier<0>();
+  if constexpr (PW == 2) {  // 128-column tiles run unsplit (the host checks)
   if (splits > 1) {
     // Split K: every workgroup of the tile publishes its partial sums (in
     // register order, so each lane later reads back exactly what it wrote) and
@@ -924,6 +943,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     if (threadIdx.x == 0)  // ready for the next launch
       __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
+  }
   // The tile leaves through LDS one m-tile (32 rows) at a time: all waves
   // write their columns of m-tile i, meet, and each stores 8 of its rows
   // while the next m-tile is converted, so the stores (the HBM write rate
@@ -963,14 +983,16 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     }
     return;
   }
-  const uint32_t n = p0 * kPanelRows + r * 8;
+  // a row of the tile is 16 PW lanes' 16 bytes, a store instruction 4 / PW rows
+  constexpr uint32_t kLanesPerRow = 16 * PW, kRowsPerStore = 4 / PW;
+  const uint32_t n = p0 * kPanelRows + (lane % kLanesPerRow) * 8;
   const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
       static_cast<f16 *>(Cout) + (size_t)m0 * N, 0, (int)(rows * N * 2), 0x00020000);
-  f32x4 b4[2][4];
+  f32x4 b4[PW][4];
   if constexpr (EPI != MADI_EPI_NONE) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      uint32_t pb = p0 + 2 * wave + t;
+    for (int t = 0; t < PW; ++t) {
+      uint32_t pb = p0 + PW * wave + t;
       pb = pb < np ? pb : np - 1;  // clamped panels: bias read in bounds, result never stored
 #pragma unroll
       for (int g = 0; g < 4; ++g)
@@ -980,8 +1002,8 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
 #pragma unroll
   for (int i = 0; i < MT; ++i) {
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint32_t nl = (2 * wave + t) * kPanelRows;  // tile-local column of the panel
+    for (int t = 0; t < PW; ++t) {
+      const uint32_t nl = (PW * wave + t) * kPanelRows;  // tile-local column of the panel
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         float v[4] = {acc[t][i][g * 4 + 0], acc[t][i][g * 4 + 1], acc[t][i][g * 4 + 2],
@@ -997,14 +1019,15 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
           }
         }
         const f16x4 o = {(f16)v[0], (f16)v[1], (f16)v[2], (f16)v[3]};
-        *reinterpret_cast<f16x4 *>(Ct + (i * 32 + r) * kCStride + (nl + g * 8 + h * 4) * 2) = o;
+        *reinterpret_cast<f16x4 *>(Ct + (i * 32 + r) * G::kCPitch + (nl + g * 8 + h * 4) * 2) = o;
       }
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const uint32_t row = i * 32 + wave * 8 + 2 * j + h;
-      const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * kCStride + r * 16);
+    for (int j = 0; j < 2 * PW; ++j) {
+      const uint32_t row = i * 32 + wave * 8 + kRowsPerStore * j + lane / kLanesPerRow;
+      const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * G::kCPitch +
+                                                       (lane % kLanesPerRow) * 16);
       if (n < N) __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * N + n) * 2, 0, kSc1);
     }
   }
@@ -1592,8 +1615,16 @@ uint32_t split_count(uint32_t tiles, uint32_t chunks) {
   return splits < 1 ? 1 : splits;
 }
 
-uint32_t tile_count(uint32_t M, uint32_t N, uint32_t MT) {
-  return (M + 32 * MT - 1) / (32 * MT) * ((N + 255) / 256);
+uint32_t tile_count(uint32_t M, uint32_t N, uint32_t MT, uint32_t PW = 2) {
+  return (M + 32 * MT - 1) / (32 * MT) * ((N + 128 * PW - 1) / (128 * PW));
+}
+
+// 128-column tiles take unpadded K loops only (a multiple of four chunks, at
+// least eight); MADI_GEMM_NARROW=0 keeps 256-column tiles everywhere.
+bool narrow_ok(uint32_t K) {
+  const uint32_t chunks = K / kChunkK;
+  const char *e = getenv("MADI_GEMM_NARROW");
+  return chunks % 4 == 0 && chunks >= 8 && !(e && e[0] == '0');
 }
 
 // ---- fixed scratch for the allocation-free entry point.  A K split's
@@ -1652,11 +1683,11 @@ bool use_tail(uint32_t splits) {
 // Where a launch keeps its split-K partials and counters.
 enum Scratch { kWorkspace = 0, kStatic = 1 };
 
-template <int MT, int EPI, bool F32 = false>
+template <int MT, int EPI, bool F32 = false, int PW = 2>
 int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const float *bias,
                 uint32_t M, uint32_t N, uint32_t K, Scratch where) {
   const uint32_t tiles_m = (M + 32 * MT - 1) / (32 * MT);
-  const uint32_t tiles_n = (N + 255) / 256;
+  const uint32_t tiles_n = (N + 128 * PW - 1) / (128 * PW);
   const uint32_t group_m = tiles_m < 6 ? tiles_m : 6;
   const uint32_t T = tiles_m * tiles_n, chunks = K / kChunkK;
   const uint32_t splits = split_count(T, chunks);
@@ -1687,7 +1718,14 @@ int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const 
     if (n == cper + 1 && crem == 0) continue;
     if (n % WD || n < 2 * WD) padded = true;
   }
-  if (padded)
+  if constexpr (PW == 1) {
+    // 128-column tiles: the host chooses them only for unpadded, unsplit shapes
+    if (padded || splits != 1)
+      return fail(MADI_ERR_SHAPE, "madi_q8_gemm: 128-column tiles need an unsplit, unpadded K loop");
+    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false, false, false, 1>), dim3(T), dim3(kWaves * 64),
+                       0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
+                       bias, ws, cnt);
+  } else if (padded)
     hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, true, F32>), dim3(T, splits), dim3(kWaves * 64),
                        0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
                        bias, ws, cnt);
@@ -1707,14 +1745,16 @@ int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const 
   return check_launch(F32 ? "madi_q8_pproj" : "madi_q8_gemm");
 }
 
-template <int MT>
+template <int MT, int PW = 2>
 int dispatch_epi(int epi, const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C,
                  const float *bias, uint32_t M, uint32_t N, uint32_t K, Scratch where) {
   switch (epi) {
-  case MADI_EPI_NONE: return launch_gemm<MT, MADI_EPI_NONE>(A, qs, sc, C, bias, M, N, K, where);
-  case MADI_EPI_BIAS: return launch_gemm<MT, MADI_EPI_BIAS>(A, qs, sc, C, bias, M, N, K, where);
+  case MADI_EPI_NONE:
+    return launch_gemm<MT, MADI_EPI_NONE, false, PW>(A, qs, sc, C, bias, M, N, K, where);
+  case MADI_EPI_BIAS:
+    return launch_gemm<MT, MADI_EPI_BIAS, false, PW>(A, qs, sc, C, bias, M, N, K, where);
   case MADI_EPI_BIAS_GELU:
-    return launch_gemm<MT, MADI_EPI_BIAS_GELU>(A, qs, sc, C, bias, M, N, K, where);
+    return launch_gemm<MT, MADI_EPI_BIAS_GELU, false, PW>(A, qs, sc, C, bias, M, N, K, where);
   default: return fail(MADI_ERR_ARG, "madi_q8_gemm: unknown epilogue %d", epi);
   }
 }
@@ -1767,8 +1807,22 @@ int q8_gemm(const char *what, const void *a, const void *qs, const void *scales,
   // cross K,V 1280->2560 120 -> 240 tiles (18.2 -> 13.9 us); q,k,v
   // 1280->3840 (180 tiles) and fc1 (240) keep 128 rows.
   const uint32_t cus = (uint32_t)cu_count();
-  if (tile_count(m, n, 1) <= cus) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k, where);
-  if (tile_count(m, n, 2) <= cus) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  // Where that tile would be 32 or 64 rows, a twice-as-tall tile of 128
+  // columns (four waves of one panel each) keeps the tile count and halves
+  // the dequantisation per MFMA (it scales as 1 / tile height): out-proj
+  // 1280 -> 1280 at M = 1500 runs 64 x 128 tiles, cross K|V 1280 -> 2560
+  // 128 x 128 tiles.  K loops that are padded stay with 256-column tiles.
+  const bool narrow = narrow_ok(k);
+  if (tile_count(m, n, 1) <= cus) {
+    if (narrow && tile_count(m, n, 2, 1) <= cus)
+      return dispatch_epi<2, 1>(epilogue, A, Q, S, C, bias, m, n, k, where);
+    return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  }
+  if (tile_count(m, n, 2) <= cus) {
+    if (narrow && tile_count(m, n, 4, 1) <= cus)
+      return dispatch_epi<4, 1>(epilogue, A, Q, S, C, bias, m, n, k, where);
+    return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  }
   if (tile_count(m, n, 3) <= cus) return dispatch_epi<3>(epilogue, A, Q, S, C, bias, m, n, k, where);
   // at least two rounds of 128-row tiles: the persistent tile loop
   if (persist_ok(m, n, k)) {

@@ -376,6 +376,45 @@ def test_gemm_tail_matches_chunk_loop(q, m, n, k, epi):
     assert np.all(np.isfinite(c_tail))
 
 
+@pytest.mark.parametrize("m,n,k,epi", [
+    (1500, 1280, 1280, O.EPI_NONE),       # out-proj: 64 x 128 tiles (24 x 10)
+    (1500, 1280, 1280, O.EPI_BIAS_GELU),
+    (1500, 2560, 1280, O.EPI_BIAS),       # cross K|V: 128 x 128 tiles (12 x 20)
+    (1500, 2560, 1280, O.EPI_BIAS_GELU),
+    (130, 320, 768, O.EPI_BIAS),          # a 2-row last m-tile, columns past N
+    (200, 992, 512, O.EPI_NONE),          # 31 panels: the last tile has three
+])
+def test_gemm_narrow_tiles_match_wide(q, m, n, k, epi):
+    """128-column tiles (one panel per wave, twice the rows) against the
+    256-column tiles of the same shape (MADI_GEMM_NARROW=0): every output
+    accumulates the same MFMAs in the same order, so the bits agree; the
+    oracle checks a row sample, element-wise."""
+    import os
+    say(f"gemm narrow vs wide m={m} n={n} k={k} epi={epi}")
+    a, qs, sc = synth.gemm_case(m + 5 * n + k, m, n, k)
+    bias = np.random.default_rng(n).standard_normal(n).astype(np.float32)
+    b = None if epi == O.EPI_NONE else bias
+    gelu = epi == O.EPI_BIAS_GELU
+    old = os.environ.pop("MADI_GEMM_NARROW", None)
+    try:
+        c_narrow = _gemm(q, a, qs, sc, bias=b, gelu=gelu)
+        os.environ["MADI_GEMM_NARROW"] = "0"
+        c_wide = _gemm(q, a, qs, sc, bias=b, gelu=gelu)
+    finally:
+        os.environ.pop("MADI_GEMM_NARROW", None)
+        if old is not None:
+            os.environ["MADI_GEMM_NARROW"] = old
+    assert np.array_equal(c_narrow.view(np.uint16), c_wide.view(np.uint16))
+    rows = tile_rows(m)
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, bias=b, epilogue=epi, threads=16)
+    assert normwise(c_narrow[rows], ref) <= TOL
+    if b is None:
+        assert tight_ok(c_narrow[rows], a[rows], qs, sc)
+    else:
+        assert tight_epi_ok(c_narrow[rows], a[rows], qs, sc, bias, gelu)
+    assert np.all(np.isfinite(c_narrow))
+
+
 @pytest.mark.parametrize("name,n,k", [("fc1", 5120, 1280), ("fc2", 1280, 5120)])
 def test_gemm_long_audio_full_m(q, name, n, k):
     """16 stacked windows, M = 24000: 128-row tiles, 188 x 20 (fc1) and 188 x 5
