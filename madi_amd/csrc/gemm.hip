@@ -6,11 +6,14 @@
 // mul_mm_q8 (kernels/q8_gemm.metal:29-102) and m4_gemm_q8_bias_gelu
 // (kernels/m4_gemm.metal:131-189).
 //
-// Workgroup tile: 256 weight rows (8 panels) x 32*MT activation rows, four
-// waves, one per SIMD.  Wave w owns panels 2w, 2w+1 and all MT m-tiles, so per
-// 16-wide k-step it runs 2*MT independent 32x32x16 MFMAs on two dequantised
-// weight fragments and MT activation fragments.  The weight is the MFMA A
-// operand (rows = n) and the activations the B operand (columns = m).
+// Workgroup tile: 128*PW weight rows (4*PW panels) x 32*MT activation rows,
+// four waves, one per SIMD.  Wave w owns panels PW*w .. PW*w + PW-1 and all MT
+// m-tiles, so per 16-wide k-step it runs PW*MT independent 32x32x16 MFMAs on
+// PW dequantised weight fragments and MT activation fragments.  PW = 2 (256
+// columns) by default; PW = 1 (128 columns) where it allows twice the tile
+// height at the same tile count, since the dequantisation per MFMA scales as
+// 1 / MT.  The weight is the MFMA A operand (rows = n) and the activations the
+// B operand (columns = m).
 //
 // Data movement per 64-wide K chunk:
 //   weights  each wave streams its own two panels straight into VGPRs
@@ -49,7 +52,10 @@
 // pattern every chunk, which keeps every vmcnt wait a constant.
 //
 // Tile height: 32, 64, 96 or 128 rows (MT = 1..4), chosen per shape by the
-// host so the tile count fills the CUs in one round where it can.
+// host so the tile count fills the CUs in one round where it can.  With one
+// K split and an unpadded loop the last four chunks run m-tile by m-tile
+// (tail(), below), so that the stores of finished m-tiles overlap the MFMAs
+// of the others.
 //
 // Split K: when the tiles alone cannot fill the GPU and K is long (fc2,
 // 5120 -> 1280 at M = 1500: 120 tiles of 64 rows), up to four workgroups
@@ -61,7 +67,7 @@
 // Epilogue: bias / GELU in fp32 registers, one rounding to f16, then the tile
 // leaves through LDS one 32-row m-tile at a time (the stores of one m-tile
 // overlap the conversion of the next), transposed so every global store
-// writes whole 512-byte row segments (16 bytes per lane).
+// writes whole row segments of the tile (256 or 512 bytes, 16 per lane).
 #include "common.h"
 #include "vmem.h"
 
