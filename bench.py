@@ -143,8 +143,14 @@ DEC_SHAPES = [("self_qkv", 3840, 1280), ("self_out", 1280, 1280), ("cross_q", 12
 
 
 def _timed(torch, stream, fn, reps):
-    """Average seconds per call of fn() over `reps` back-to-back calls."""
+    """Average seconds per call of fn() over `reps` back-to-back calls, after
+    untimed calls with the last min(reps, 8) indices (the first shape of a
+    configuration otherwise pays for the clocks ramping up after the set-up's
+    copies; the timed calls then start with the weight copy used longest ago,
+    as in the steady state of the rotation)."""
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for i in range(max(reps - 8, 0), reps):
+        fn(i)
     torch.cuda.synchronize()
     e0.record(stream)
     for i in range(reps):

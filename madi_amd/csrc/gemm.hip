@@ -94,7 +94,7 @@ struct Geometry {
   static constexpr int kRing = NA * kStage;
   static constexpr int kTilePanels = 4 * PW;  // panels (32 columns each) per tile
   static constexpr int kCPitch =
-      F32 ? kPanelsPerTile * kPanelRows * 4 + 16 : kTilePanels * kPanelRows * 2 + 16;
+      kTilePanels * kPanelRows * (F32 ? 4 : 2) + 16;
   static constexpr int kCTile = 32 * MT * kCPitch;
   static constexpr int kLds = kRing > kCTile ? kRing : kCTile;
   // vector-memory instructions per wave per chunk, spread over the four
@@ -698,32 +698,39 @@ __device__ inline void tail(uint8_t *smem, uint32_t c, uint32_t h, uint32_t r, u
 template <int MT, int EPI, bool PADDED, bool F32 = false, bool TAIL = false, int PW = 2>
 __global__ __launch_bounds__(256) void q8_gemm_kernel(
     const void *__restrict__ A, const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
-    uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m, uint32_t tiles_n, uint32_t group_m,
+    uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m, uint32_t tiles_n, uint32_t splits,
     uint32_t cper, uint32_t crem, void *__restrict__ Cout, const float *__restrict__ bias,
     float *__restrict__ ws, uint32_t *__restrict__ cnt) {
   using G = Geometry<MT, F32, PW>;
   static_assert(!F32 || EPI == MADI_EPI_NONE, "f32 output has no bias epilogue");
   static_assert(!TAIL || (!PADDED && !F32 && MT >= 2 && PW == 2), "the m-tile-major tail's shapes");
-  static_assert(PW == 2 || (!PADDED && !F32), "128-column tiles: unpadded f16 launches");
+  static_assert(PW == 2 || !PADDED, "128-column tiles: unpadded launches");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[G::kLds];
   __shared__ uint32_t arrived;
 
-  // ---- tile order: consecutive workgroups go to different XCDs (round-robin,
-  // x fastest), so renumber x to give each XCD a contiguous run, then walk
-  // that run in groups of `group_m` M-tiles so an XCD's tiles share A rows
-  // and W panels in its own L2.  The grid's y index is the K split: split s
-  // covers chunks [s * cper + min(s, crem), + cper + (s < crem)) of the
-  // tile.  The arguments the mapping needs come first and arrive preloaded
-  // in SGPRs; C, the bias and the split-K workspace, needed only at the end,
-  // follow.
+  // ---- tile order: consecutive workgroups go to different XCDs (round-robin),
+  // so the work items are renumbered to give each XCD a contiguous run.  The
+  // W = T * splits items (item tile * splits + split) are cut into eight runs
+  // whose lengths differ by at most one; the grid is W rounded up to a
+  // multiple of 8, workgroup L runs on XCD L % 8 and takes the (L / 8)-th item
+  // of that XCD's run, or exits past its end.  An XCD thus holds every K
+  // split of consecutive tiles, walked in groups of `group_m` M-tiles, so its
+  // tiles share A rows and W panels in its own L2.  (Measured against a
+  // split-major order, where an XCD holds consecutive tiles of one K range,
+  // and against the plain round-robin order: as fast or faster on every
+  // shape, e.g. FFN down 5120 -> 1280 at M = 320 f32 15.3 / 15.7 / 17.8 us,
+  // 24000 x 5120 -> 1280 f16 280 / 282 / 297 us.)  Split s covers chunks [s * cper + min(s, crem), + cper +
+  // (s < crem)) of the tile.  The arguments the mapping needs come first and
+  // arrive preloaded in SGPRs (the first 14 dwords); C, the bias and the
+  // split-K workspace, needed only at the end, follow.
   const uint32_t T = tiles_m * tiles_n;
-  // (a mask, not a branch: at a branch the compiler copies the kernel
-  // arguments still being loaded, which waits for them)
-  const uint32_t bid_x = blockIdx.x;
-  const uint32_t remap = 0u - (uint32_t)((T & 7) == 0);  // all ones when T % 8 == 0
-  const uint32_t bid = (((bid_x & 7) * (T >> 3) + (bid_x >> 3)) & remap) | (bid_x & ~remap);
-  const uint32_t split = blockIdx.y, splits = gridDim.y;
+  const uint32_t W = T * splits, L = blockIdx.x, x = L & 7;
+  const uint32_t first = (x * W) >> 3, run = (((x + 1) * W) >> 3) - first;
+  if ((L >> 3) >= run) return;
+  const uint32_t item = first + (L >> 3);
+  const uint32_t bid = item / splits, split = item - bid * splits;
   const uint32_t tile = bid;
+  const uint32_t group_m = tiles_m < 6 ? tiles_m : 6;
   const uint32_t per_group = group_m * tiles_n;
   const uint32_t gi = bid / per_group, first_m = gi * group_m;
   const uint32_t gm = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
@@ -846,7 +853,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   // n = 32(PW w + t) + 8g + 4h + e (acc[t][i][4g + e]).  Every wave must finish
   // reading the ring before it becomes the C tile.
   wait_then_barrier<0>();
-  if constexpr (PW == 2) {  // 128-column tiles run unsplit (the host checks)
+  // f16 launches of 128-column tiles run unsplit (the host checks), and leave
+  // the reduction's registers out of their allocation
+  constexpr bool kSplits = PW == 2 || F32;
+  if constexpr (kSplits) {
   if (splits > 1) {
     // Split K: every workgroup of the tile publishes its partial sums (in
     // register order, so each lane later reads back exactly what it wrote) and
@@ -855,11 +865,11 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     // device-scope (sc1) buffer accesses, which write through and read past
     // the XCD's own L2, and the count is a system-scope atomic, so no L2-wide
     // writeback or invalidate is needed.
-    constexpr uint32_t kPart = 4 * 2 * MT * 4 * 64 * 16;  // bytes per partial tile
+    constexpr uint32_t kPart = 4 * PW * MT * 4 * 64 * 16;  // bytes per partial tile
     const __amdgpu_buffer_rsrc_t wsr =
         __builtin_amdgcn_make_buffer_rsrc(ws, 0, (int)(T * splits * kPart), 0x00020000);
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < PW; ++t)
 #pragma unroll
       for (int i = 0; i < MT; ++i)
 #pragma unroll
@@ -867,7 +877,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
           __builtin_amdgcn_raw_buffer_store_b128(
               __builtin_bit_cast(u32x4, (f32x4){acc[t][i][4 * g], acc[t][i][4 * g + 1],
                                                 acc[t][i][4 * g + 2], acc[t][i][4 * g + 3]}),
-              wsr, ((((wave * 2 + t) * MT + i) * 4 + g) * 64 + lane) * 16,
+              wsr, ((((wave * PW + t) * MT + i) * 4 + g) * 64 + lane) * 16,
               (tile * splits + split) * kPart, kSc1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial has been written through
     __syncthreads();
@@ -875,10 +885,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
       arrived = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
     __syncthreads();
     if (arrived != splits - 1) return;
-    constexpr int kGroups = 2 * MT * 4;  // register groups q = (t, i, g) in order
+    constexpr int kGroups = PW * MT * 4;  // register groups q = (t, i, g) in order
     if (MT <= 2 && splits == 2) {
       // Two splits (fc2-like shapes at 64-row tiles): the wave's whole share
-      // of the other partial (2 * MT * 4 KiB) in flight at once, one memory
+      // of the other partial (PW * MT * 4 KiB) in flight at once, one memory
       // latency; own + other is exact in either order.
       const uint32_t other = split ^ 1u;
       f32x4 o[kGroups];
@@ -963,15 +973,18 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   uint8_t *Ct = smem;
   const uint32_t rows = M - m0 < 32 * MT ? M - m0 : 32 * MT;
   if constexpr (F32) {
-    // f32 result: a 1 KiB row segment per store (lane l: columns 4l .. 4l+3)
-    const uint32_t n = p0 * kPanelRows + lane * 4;
+    // f32 result: a row of the tile is 32 PW lanes' 16 bytes (4 columns
+    // each), a store instruction 2 / PW rows
+    constexpr uint32_t kLanesPerRow = 32 * PW, kRowsPerStore = 2 / PW;
+    const uint32_t col = lane % kLanesPerRow;
+    const uint32_t n = p0 * kPanelRows + col * 4;
     const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
         static_cast<float *>(Cout) + (size_t)m0 * N, 0, (int)(rows * N * 4), 0x00020000);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const uint32_t nl = (2 * wave + t) * kPanelRows;
+      for (int t = 0; t < PW; ++t) {
+        const uint32_t nl = (PW * wave + t) * kPanelRows;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const f32x4 o = {acc[t][i][g * 4 + 0], acc[t][i][g * 4 + 1], acc[t][i][g * 4 + 2],
@@ -981,9 +994,9 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
       }
       __syncthreads();
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t row = i * 32 + wave * 8 + j;
-        const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * G::kCPitch + lane * 16);
+      for (uint32_t j = 0; j < 8 / kRowsPerStore; ++j) {
+        const uint32_t row = i * 32 + wave * 8 + j * kRowsPerStore + lane / kLanesPerRow;
+        const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * G::kCPitch + col * 16);
         if (n < N) __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * N + n) * 4, 0, kSc1);
       }
     }
@@ -1621,6 +1634,19 @@ uint32_t split_count(uint32_t tiles, uint32_t chunks) {
   return splits < 1 ? 1 : splits;
 }
 
+// Whether a K loop of `chunks` chunks split `splits` ways needs the padded
+// kernel: every split's chunk count must be a multiple of WD and at least
+// 2*WD for the select-free loop (split s covers chunks / splits chunks, one
+// more for the first chunks % splits splits).
+bool loop_padded(uint32_t chunks, uint32_t splits) {
+  const uint32_t cper = chunks / splits, crem = chunks % splits;
+  for (const uint32_t n : {cper, cper + 1}) {
+    if (n == cper + 1 && crem == 0) continue;
+    if (n % WD || n < 2 * WD) return true;
+  }
+  return false;
+}
+
 uint32_t tile_count(uint32_t M, uint32_t N, uint32_t MT, uint32_t PW = 2) {
   return (M + 32 * MT - 1) / (32 * MT) * ((N + 128 * PW - 1) / (128 * PW));
 }
@@ -1694,13 +1720,12 @@ int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const 
                 uint32_t M, uint32_t N, uint32_t K, Scratch where) {
   const uint32_t tiles_m = (M + 32 * MT - 1) / (32 * MT);
   const uint32_t tiles_n = (N + 128 * PW - 1) / (128 * PW);
-  const uint32_t group_m = tiles_m < 6 ? tiles_m : 6;
   const uint32_t T = tiles_m * tiles_n, chunks = K / kChunkK;
   const uint32_t splits = split_count(T, chunks);
   float *ws = nullptr;
   uint32_t *cnt = nullptr;
   if (splits > 1) {
-    const size_t part = (size_t)T * splits * (4 * 2 * MT * 4 * 64 * 16);
+    const size_t part = (size_t)T * splits * (4 * PW * MT * 4 * 64 * 16);
     if (where == kStatic) {
       if (T > kScratchCounters || part > kScratchBytes - kScratchCounters * 4)
         return fail(MADI_ERR_SHAPE,
@@ -1716,38 +1741,31 @@ int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const 
       if (rc != MADI_OK) return rc;
     }
   }
-  // split s covers cper + (s < crem) chunks; every split's chunk count a
-  // multiple of WD and at least 2*WD: the select-free loop
+  // split s covers cper + (s < crem) chunks
   const uint32_t cper = chunks / splits, crem = chunks % splits;
-  bool padded = false;
-  for (const uint32_t n : {cper, cper + 1}) {
-    if (n == cper + 1 && crem == 0) continue;
-    if (n % WD || n < 2 * WD) padded = true;
-  }
+  const bool padded = loop_padded(chunks, splits);
+  // one workgroup per (tile, split), the grid rounded up to a multiple of 8
+  // (the kernel's XCD mapping)
+  const auto go = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3((T * splits + 7) & ~7u), dim3(kWaves * 64), 0, stream(), A, qs,
+                       sc, M, N, K, tiles_m, tiles_n, splits, cper, crem, C, bias, ws, cnt);
+  };
   if constexpr (PW == 1) {
-    // 128-column tiles: the host chooses them only for unpadded, unsplit shapes
-    if (padded || splits != 1)
-      return fail(MADI_ERR_SHAPE, "madi_q8_gemm: 128-column tiles need an unsplit, unpadded K loop");
-    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false, false, false, 1>), dim3(T), dim3(kWaves * 64),
-                       0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
-                       bias, ws, cnt);
+    // 128-column tiles: the host chooses them only for unpadded K loops, and
+    // for the f16 GEMM only unsplit
+    if (padded || (!F32 && splits != 1))
+      return fail(MADI_ERR_SHAPE, "%s: 128-column tiles need an unpadded%s K loop",
+                  F32 ? "madi_q8_pproj" : "madi_q8_gemm", F32 ? "" : ", unsplit");
+    go(q8_gemm_kernel<MT, EPI, false, F32, false, 1>);
   } else if (padded)
-    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, true, F32>), dim3(T, splits), dim3(kWaves * 64),
-                       0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
-                       bias, ws, cnt);
+    go(q8_gemm_kernel<MT, EPI, true, F32>);
   else if constexpr (!F32 && MT >= 2) {
     if (use_tail(splits))
-      hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false, false, true>), dim3(T, splits),
-                         dim3(kWaves * 64), 0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n,
-                         group_m, cper, crem, C, bias, ws, cnt);
+      go(q8_gemm_kernel<MT, EPI, false, false, true>);
     else
-      hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false, false>), dim3(T, splits),
-                         dim3(kWaves * 64), 0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n,
-                         group_m, cper, crem, C, bias, ws, cnt);
+      go(q8_gemm_kernel<MT, EPI, false, false>);
   } else
-    hipLaunchKernelGGL((q8_gemm_kernel<MT, EPI, false, F32>), dim3(T, splits), dim3(kWaves * 64),
-                       0, stream(), A, qs, sc, M, N, K, tiles_m, tiles_n, group_m, cper, crem, C,
-                       bias, ws, cnt);
+    go(q8_gemm_kernel<MT, EPI, false, F32>);
   return check_launch(F32 ? "madi_q8_pproj" : "madi_q8_gemm");
 }
 
@@ -1853,15 +1871,34 @@ int gemm_scratch_init() {
 
 // out[M][N] (f32) = f16(in[M][K] (f32)) . deq(W)^T through the MFMA GEMM
 // (the batched projection for many rows): 32- or 64-row tiles by the same
-// rule as the f16 GEMM.  The caller has checked the shapes (N % 32 == 0,
-// K % 64 == 0, 16-byte aligned in and out, operands below 2 GiB).
+// rule as the f16 GEMM, replaced by 128-column tiles where their K loop is
+// unpadded: where a 32-row tile would be chosen, 32 x 128 tiles if they fit
+// one per CU (twice the workgroups, each with half the work: M = 320
+// 1280 -> 2560 8.1 us against 10.1 on 64 x 128 tiles), else 64 x 128 tiles
+// (the same tile count as 32 x 256, half the dequantisation per MFMA); and
+// where K is split over workgroups, 64 x 128 tiles if they keep the split
+// count (FFN down 5120 -> 1280 at M = 320 runs 200 workgroups instead of
+// 100).  The caller has checked the shapes (N % 32 == 0, K % 64 == 0,
+// 16-byte aligned in and out, operands below 2 GiB).
 int q8_gemm_f32io(const float *in, const void *qs, const void *scales, float *out, uint32_t m,
                   uint32_t n, uint32_t k) {
   const uint8_t *Q = static_cast<const uint8_t *>(qs);
   const f16 *S = static_cast<const f16 *>(scales);
   const uint32_t cus = (uint32_t)cu_count();
-  if (m <= 32 || (tile_count(m, n, 1) <= cus && split_count(tile_count(m, n, 4), k / kChunkK) == 1))
+  if (m <= 32 || (tile_count(m, n, 1) <= cus && split_count(tile_count(m, n, 4), k / kChunkK) == 1)) {
+    if (narrow_ok(k) && tile_count(m, n, 1, 1) <= cus &&
+        split_count(tile_count(m, n, 1, 1), k / kChunkK) == 1)
+      return launch_gemm<1, MADI_EPI_NONE, true, 1>(in, Q, S, out, nullptr, m, n, k, kWorkspace);
+    if (m > 32 && narrow_ok(k) && tile_count(m, n, 2, 1) <= cus &&
+        split_count(tile_count(m, n, 2, 1), k / kChunkK) == 1)
+      return launch_gemm<2, MADI_EPI_NONE, true, 1>(in, Q, S, out, nullptr, m, n, k, kWorkspace);
     return launch_gemm<1, MADI_EPI_NONE, true>(in, Q, S, out, nullptr, m, n, k, kWorkspace);
+  }
+  const uint32_t chunks = k / kChunkK, wide = tile_count(m, n, 2), narrow = tile_count(m, n, 2, 1);
+  const uint32_t splits = split_count(narrow, chunks);
+  if (narrow_ok(k) && splits > 1 && splits == split_count(wide, chunks) && narrow * splits <= cus &&
+      !loop_padded(chunks, splits))
+    return launch_gemm<2, MADI_EPI_NONE, true, 1>(in, Q, S, out, nullptr, m, n, k, kWorkspace);
   return launch_gemm<2, MADI_EPI_NONE, true>(in, Q, S, out, nullptr, m, n, k, kWorkspace);
 }
 }  // namespace madi

@@ -354,13 +354,18 @@ extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const 
   if (int rc = deferred_before_read(in, (size_t)m * k * 4)) return rc;
   if (int rc = deferred_before_write(out, (size_t)m * n * 4)) return rc;
   // Many rows (sequence prefill): the MFMA GEMM dequantises each weight once
-  // per 32 or 64 rows of a tile that spans 256 outputs, where this kernel
-  // dequantises it once per 32-row slice of a single panel.  Its tiles take
-  // ~11 us however few rows they hold (one K loop), so it pays from 160 rows
-  // on wide or long weights; a 1280 x 1280 weight has too few tiles (measured,
-  // cold weights, M = 320: 1280->5120 12.3 vs 27.2 us, 1280->3840 12.2 vs
-  // 20.3, 5120->1280 19.0 vs 34.1, 1280->1280 11.2 vs 8.7).
-  if (m >= kGemmRows && (n >= 2048 || k >= 4096) && n % kPanelRows == 0 && aligned(in, 16) &&
+  // per 32 or 64 rows of a tile that spans 128 or 256 outputs, where this
+  // kernel dequantises it once per 32-row slice of a single panel.  Its tiles
+  // take 7.5-11 us however few rows they hold (one K loop), so it pays from
+  // 160 rows on wide or long weights, and on narrower ones once this kernel's
+  // grid (a workgroup per panel and slice) no longer fits one per CU: 1280 x
+  // 1280 at M = 192 (240 workgroups) 5.1 us here against 7.7 on the GEMM,
+  // at M = 224 (280) 8.3 against 7.7 (measured, cold weights; M = 320:
+  // 1280->5120 12.3 vs 27.2 us, 1280->3840 12.2 vs 20.3, 5120->1280 19.0 vs
+  // 34.1).
+  const uint32_t skinny_wgs = (n + kPanelRows - 1) / kPanelRows * ((m + kSlice - 1) / kSlice);
+  if (m >= kGemmRows && (n >= 2048 || k >= 4096 || skinny_wgs > (uint32_t)cu_count()) &&
+      n % kPanelRows == 0 && aligned(in, 16) &&
       aligned(out, 16) &&
       (uint64_t)m * k * 4 < (1ull << 31) && (uint64_t)n * 256 < (1ull << 31))
     return q8_gemm_f32io(in, qs, scales, out, m, n, k);

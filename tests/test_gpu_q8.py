@@ -702,7 +702,9 @@ def staged_ok(c, x, qs, sc):
     (8, 51866, 1280),    # batched vocab logits, tail panel of 26 rows
     (32, 1280, 1280), (33, 3840, 1280), (70, 1280, 5120), (5, 40, 64),
     (17, 5120, 1280),    # one 32-row slice, 15 rows past M
-    (320, 1280, 1280),   # sequence prefill at its largest M: ten slices
+    (320, 640, 1280),    # ten slices (M = 320, the prefill's largest) of 20 panels
+    (192, 1280, 1280),   # six slices of 40 panels: 240 workgroups, the most that
+                         # stay on the skinny kernel for a 1280 x 1280 weight
     # the batched decode step at M = 16: vocab (four-panel groups, tail panel),
     # q|k|v, FFN up and the 1280 x 1280 projections (single panels, unsplit)
     (16, 51866, 1280), (16, 3840, 1280), (16, 5120, 1280), (16, 1280, 1280),
@@ -719,14 +721,16 @@ def test_pproj_parity(q, m, n, k):
     assert staged_ok(c, x, qs, sc)
 
 
-# From 160 rows, for weights 2048 wide or 4096 long, the batched projection
-# runs as the MFMA GEMM with f32 activations and an f32 result
-# (q8_gemm_kernel<MT, NONE, PADDED, true>): 32-row tiles, 64-row tiles, an
-# M tail, a padded K loop (5 chunks over 4096 outputs) and the 5120-wide K
-# split over workgroups; 1280 x 1280 stays on the skinny kernel.
+# From 160 rows, for weights 2048 wide or 4096 long, or where the skinny
+# kernel's grid (panels x 32-row slices) exceeds the CUs, the batched
+# projection runs as the MFMA GEMM with f32 activations and an f32 result
+# (q8_gemm_kernel<MT, NONE, PADDED, true, false, PW>): 32 x 128, 64 x 128 and
+# 64 x 256 tiles, an M tail, a padded K loop (5 chunks over 4096 outputs) and
+# the 5120-wide K split over workgroups; 1280 x 1280 from 224 rows.
 @pytest.mark.parametrize("m,n,k", [
     (160, 5120, 1280), (320, 3840, 1280), (320, 5120, 1280), (161, 4096, 320),
-    (320, 1280, 5120), (700, 2560, 1280), (256, 1280, 1280),
+    (320, 1280, 5120), (700, 2560, 1280), (256, 1280, 1280), (224, 1280, 1280),
+    (320, 1280, 1280),
 ])
 def test_pproj_many_rows_gemm(q, m, n, k):
     say(f"pproj (GEMM) m={m} n={n} k={k}")
@@ -738,6 +742,43 @@ def test_pproj_many_rows_gemm(q, m, n, k):
     ref = O.q8_proj(x, qs, sc, threads=16)
     assert normwise(c, ref) <= TOL, normwise(c, ref)
     assert staged_ok(c, x, qs, sc)
+
+
+# Where the batched projection would run 32-row tiles, or 64-row tiles with K
+# split four ways over workgroups, and the K loop is unpadded, it runs
+# 32 x 128 or 64 x 128 tiles (one panel per wave): the same MFMAs per output
+# in the same order and the same splits summed in the same order, so the f32
+# results equal the 256-column tiles' (MADI_GEMM_NARROW=0) bit for bit.
+# Shapes: the prefill's q|k|v, FFN up and FFN down (four splits) at M = 320
+# (64 x 128), its 1280 x 1280 projections and cross K|V (32 x 128), FFN up at
+# M = 160 (32 x 128), an M tail of 33 rows, 65 panels (the last tile holds one
+# valid panel and three clamped ones), and FFN down at M = 160 (a 32-row tail
+# in a 64-row tile).
+@pytest.mark.parametrize("m,n,k", [
+    (320, 3840, 1280), (320, 5120, 1280), (161, 2048, 512), (320, 2080, 1280),
+    (320, 1280, 5120), (160, 1280, 5120), (320, 1280, 1280), (320, 2560, 1280),
+    (160, 5120, 1280),
+])
+def test_pproj_narrow_tiles_match_wide(q, m, n, k):
+    import os
+    say(f"pproj (GEMM) narrow vs wide m={m} n={n} k={k}")
+    rng = np.random.default_rng(m * 11 + n + k)
+    x = (rng.standard_normal((m, k)) * 3).astype(np.float32)
+    qs, sc = synth.q8_weight(rng, n, k)
+    old = os.environ.pop("MADI_GEMM_NARROW", None)
+    try:
+        c_narrow = _pproj(q, x, qs, sc)
+        os.environ["MADI_GEMM_NARROW"] = "0"
+        c_wide = _pproj(q, x, qs, sc)
+    finally:
+        os.environ.pop("MADI_GEMM_NARROW", None)
+        if old is not None:
+            os.environ["MADI_GEMM_NARROW"] = old
+    assert np.all(np.isfinite(c_narrow))
+    assert np.array_equal(c_narrow.view(np.uint32), c_wide.view(np.uint32))
+    ref = O.q8_proj(x, qs, sc, threads=16)
+    assert normwise(c_narrow, ref) <= TOL, normwise(c_narrow, ref)
+    assert staged_ok(c_narrow, x, qs, sc)
 
 
 def test_pproj_many_rows_one_hot(q):
