@@ -13,8 +13,8 @@
 // the result away from the fp32 reference of test_batchproj.zig:72-78).
 //
 // Workgroup: P weight panels (32 rows each; P = 4 for the 51866-row vocab
-// matrix, 1 otherwise) x one slice of 32 activation rows (the MFMA columns),
-// KW waves splitting K.  Per 64-wide K chunk a wave loads each panel's two
+// matrix with 32-row slices, 1 otherwise) x one slice of 32 activation rows
+// (the MFMA columns), KW waves splitting K.  Per 64-wide K chunk a wave loads each panel's two
 // 16-byte units per lane (lane (h, r): row r's 32 weights of quantisation
 // block h) and scale, and the slice's first XR rows (8, 16 or 32: the rows a
 // batch of M <= XR has) of 64 f32 activations with coalesced loads (each
@@ -280,10 +280,15 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 
 // waves split K, three chunks in flight each, so a K = 1280 range (2 - 3
 // chunks per wave) is one round of loads.  (Sixteen waves with two chunks
 // each measured slower: a workgroup's waves start up to ~0.8 us apart and the
-// reduction waits for the last.)  Panel groups (the vocab logits, 1621
-// panels): four panels per wave share each activation load, four waves split
-// K.
+// reduction waits for the last.)  The vocab logits (1621 panels) up to 16
+// rows: one panel per workgroup and four waves splitting K, two chunks in
+// flight each; 1621 workgroups spread evenly over the CUs, where 406 groups
+// of four panels leave a second, partial round (M = 8: 12.6 against 14.6 us,
+// M = 16: 14.2 against 15.5).  With 32-row slices the activations of a chunk
+// are four times the weight bytes, and four panels per workgroup sharing each
+// activation load stay ahead (M = 32: 17.2 against 19.5 us).
 constexpr int kPanelWaves = 8, kPanelWin = 3;
+constexpr int kVocabWaves = 4, kVocabWin = 2;
 constexpr int kGroupWaves = 4, kGroupWin = 2;
 constexpr uint32_t kMaxSplits = 4;
 
@@ -319,12 +324,16 @@ int launch_skinny(const Proj &a) {
   return check_launch("madi_q8_pproj");
 }
 
-// wide matrices (the vocab logits): four panels per workgroup share each
-// activation load; narrow ones keep one panel per workgroup
+// wide matrices (the vocab logits): one panel per workgroup up to 16 rows,
+// four panels sharing each activation load for 32-row slices; narrow ones
+// keep one panel per workgroup with eight waves
 template <int XR>
 int launch_rows(const Proj &a) {
   const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
-  if (np >= 1024) return launch_skinny<4, kGroupWaves, XR, kGroupWin>(a);
+  if (np >= 1024) {
+    if constexpr (XR <= 16) return launch_skinny<1, kVocabWaves, XR, kVocabWin>(a);
+    return launch_skinny<4, kGroupWaves, XR, kGroupWin>(a);
+  }
   return launch_skinny<1, kPanelWaves, XR, kPanelWin>(a);
 }
 
