@@ -106,5 +106,15 @@ def check(rc: int, what: str) -> None:
         raise MadiError(rc, what, last_error())
 
 
+_FNS: dict = {}
+
+
 def call(name: str, *args) -> None:
-    check(getattr(lib(), name)(*args), name)
+    """Call export `name` and raise MadiError on a nonzero code (the function
+    objects are looked up once: this is on every launch's host path)."""
+    fn = _FNS.get(name)
+    if fn is None:
+        fn = _FNS[name] = getattr(lib(), name)
+    rc = fn(*args)
+    if rc != MADI_OK:
+        raise MadiError(rc, name, last_error())

@@ -24,9 +24,7 @@ NH = 20           # encoder.zig:13 (attention heads, head dim 64: encoder.zig:14
 
 
 def ptr(t) -> int | None:
-    if t is None:
-        return None
-    if isinstance(t, int):
+    if t is None or isinstance(t, int):
         return t
     return t.data_ptr()
 
