@@ -372,8 +372,8 @@ extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const 
   // at M = 224 (280) 8.3 against 7.7 (measured, cold weights; M = 320:
   // 1280->5120 12.3 vs 27.2 us, 1280->3840 12.2 vs 20.3, 5120->1280 19.0 vs
   // 34.1).
-  const uint32_t skinny_wgs = (n + kPanelRows - 1) / kPanelRows * ((m + kSlice - 1) / kSlice);
-  if (m >= kGemmRows && (n >= 2048 || k >= 4096 || skinny_wgs > (uint32_t)cu_count()) &&
+  const uint64_t skinny_wgs = (uint64_t)((n + kPanelRows - 1) / kPanelRows) * ((m + kSlice - 1) / kSlice);
+  if (m >= kGemmRows && (n >= 2048 || k >= 4096 || skinny_wgs > (uint64_t)cu_count()) &&
       n % kPanelRows == 0 && aligned(in, 16) &&
       aligned(out, 16) &&
       (uint64_t)m * k * 4 < (1ull << 31) && (uint64_t)n * 256 < (1ull << 31))
