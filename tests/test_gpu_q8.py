@@ -754,12 +754,13 @@ def test_pproj_many_rows_gemm(q, m, n, k):
 # (64 x 128), its 1280 x 1280 projections and cross K|V (32 x 128), FFN up at
 # M = 160 (32 x 128), an M tail of 33 rows, 65 panels (the last tile holds one
 # valid panel and three clamped ones), FFN down at M = 160 (a 32-row tail
-# in a 64-row tile), and 1280 x 1280 at M = 231 (a 7-row tail in a 32-row
-# tile).
+# in a 64-row tile), 1280 x 1280 at M = 231 (a 7-row tail in a 32-row
+# tile), and a 96-wide weight with K = 4096 (one tile of three panels and a
+# clamped fourth, K split four ways).
 @pytest.mark.parametrize("m,n,k", [
     (320, 3840, 1280), (320, 5120, 1280), (161, 2048, 512), (320, 2080, 1280),
     (320, 1280, 5120), (160, 1280, 5120), (320, 1280, 1280), (320, 2560, 1280),
-    (160, 5120, 1280), (231, 1280, 1280),
+    (160, 5120, 1280), (231, 1280, 1280), (300, 96, 4096),
 ])
 def test_pproj_narrow_tiles_match_wide(q, m, n, k):
     import os
