@@ -57,12 +57,15 @@
 // (tail(), below), so that the stores of finished m-tiles overlap the MFMAs
 // of the others.
 //
-// Split K: when the tiles alone cannot fill the GPU and K is long (fc2,
-// 5120 -> 1280 at M = 1500: 120 tiles of 64 rows), up to four workgroups
-// share a tile, each over a contiguous K range (the grid's y index).  Each
-// publishes its fp32 partial tile to the library's workspace and counts
-// itself in with a system-scope atomic; the last to arrive adds the partials
-// in split order and runs the epilogue.
+// Split K: when the tiles alone cannot fill the GPU and K is long and the
+// in-workgroup K split (q8_gemm_ks_kernel, below) does not take the shape
+// (700 x 5120 -> 1280: 55 tiles of 64 x 256; the batched projection's FFN
+// down at M = 320: 50 tiles of 64 x 128), up to four workgroups share a tile,
+// each over a contiguous K range.  Each publishes its fp32 partial tile to
+// the library's workspace and counts itself in with a system-scope atomic;
+// the last to arrive adds the partials in split order and runs the epilogue.
+// The grid is one-dimensional over (tile, split) items, renumbered so that
+// each XCD runs a contiguous share of them (the tile order, below).
 //
 // Epilogue: bias / GELU in fp32 registers, one rounding to f16, then the tile
 // leaves through LDS one 32-row m-tile at a time (the stores of one m-tile
