@@ -189,7 +189,10 @@ int madi_q8_gemv_f16x(float *out, const void *x_f16, const void *qs, const void 
                       const float *bias, uint32_t n, uint32_t k, int epilogue);
 
 /* Batched / skinny projection: out[M][N] (f32) = in[M][K] (f32) . deq(W)^T for
- * a few token rows (the batched-decode GEMV; any M, 32 rows per pass over W).
+ * any M: a few token rows (the batched-decode GEMV, 32 rows per pass over W)
+ * or, from 160 rows on weights 2048 or more wide or 4096 or more long, or
+ * where the row count would need more workgroups than CUs, the MFMA GEMM with
+ * f32 operands (sequence prefill); the same arithmetic either way.
  * Replaces pproj (engine/metal/decoder.zig:427-432: kDeq + kCvt32 +
  * matmulF16Batched + kCvt16) and the per-slot proj calls of the batched
  * decode (decoder.zig:337-341) with one fused kernel: activations rounded to
