@@ -468,7 +468,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (--gpus {args.gpus} requested): the Q8 matmul "
-              "path runs on a single MI355X; see DESIGN.md for how it would shard.",
+              "path is built and measured on a single MI355X (one GPU's share of the work); "
+              "sharding it over several GPUs is a design, not a built path.",
               file=sys.stderr)
         sys.exit(2)
 
