@@ -860,8 +860,9 @@ def test_graph_replay_decode_sequence(q):
 def test_graph_replay_after_workspace_growth(q):
     """Split-K launches captured while the workspace holds its initial 4 MiB
     (a fresh library: madi_cleanup then madi_init), then an eager split GEMM
-    that needs 15.7 MB grows it: the outgrown buffer stays allocated, so the
-    graph's kernels, which still name it, replay to the eager results."""
+    that needs 15.7 MB grows it (1000 x 5120 -> 1280: 80 tiles of 64 x 256,
+    three K splits): the outgrown buffer stays allocated, so the graph's
+    kernels, which still name it, replay to the eager results."""
     say("graph replay after workspace growth")
     from madi_amd import _lib
     _lib.lib().madi_cleanup()
@@ -894,13 +895,13 @@ def test_graph_replay_after_workspace_growth(q):
             q.init(side)
             seq()
     q.init()
-    # fc2 at M = 1500 (two splits of 120 tiles) grows the workspace past 4 MiB
-    a3, qs3, sc3 = synth.gemm_case(38, 1500, 1280, 5120)
+    # 1000 x 5120 -> 1280 (three splits of 80 tiles) grows the workspace past 4 MiB
+    a3, qs3, sc3 = synth.gemm_case(38, 1000, 1280, 5120)
     w3 = q.upload_q8(qs3, sc3)
-    c3 = torch.empty((1500, 1280), dtype=torch.int16, device="cuda")
-    q.kGemmQ8(dev_f16(a3), w3, c3, 1500, 1280, 5120)
+    c3 = torch.empty((1000, 1280), dtype=torch.int16, device="cuda")
+    q.kGemmQ8(dev_f16(a3), w3, c3, 1000, 1280, 5120)
     q.sync()
-    rows = tile_rows(1500)
+    rows = tile_rows(1000)
     assert normwise(host_f16(c3)[rows], O.q8_gemm_rows(a3, qs3, sc3, rows=rows, threads=8)) <= TOL
     for rep in range(3):
         for t in (o1, o2):

@@ -42,11 +42,13 @@ def run(q, name, a_d, w, bias_d, m, n, k, epi):
     return c.cpu().numpy()
 
 
-# (m, n, k, epilogue): fc2 + bias at M = 1500 (120 tiles of 64 rows, two K
-# splits: 15 MiB of partials), then smaller split shapes (four splits over 45
-# and 2 tiles), then a shape that does not split at all
-CASES = [(1500, 1280, 5120, _lib.EPI_BIAS), (257, 1280, 5120, _lib.EPI_NONE),
-         (20, 512, 4096, _lib.EPI_BIAS_GELU), (96, 512, 1280, _lib.EPI_BIAS_GELU)]
+# (m, n, k, epilogue): 1000 x 5120 -> 1280 + bias (80 tiles of 64 x 256,
+# three K splits: 15.7 MB of partials), then smaller split shapes (four
+# splits over 25 and 2 tiles), then a shape that does not split at all, and
+# fc2 + bias at M = 1500, whose K split stays inside the workgroup (no scratch)
+CASES = [(1000, 1280, 5120, _lib.EPI_BIAS), (257, 1280, 5120, _lib.EPI_NONE),
+         (20, 512, 4096, _lib.EPI_BIAS_GELU), (96, 512, 1280, _lib.EPI_BIAS_GELU),
+         (1500, 1280, 5120, _lib.EPI_BIAS)]
 
 
 def test_noalloc_matches_gemm_two_calls(q):
