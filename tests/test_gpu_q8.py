@@ -706,7 +706,7 @@ def staged_ok(c, x, qs, sc):
     (320, 640, 1280),    # ten slices (M = 320, the prefill's largest) of 20 panels
     (192, 1280, 1280),   # six slices of 40 panels: 240 workgroups, the most that
                          # stay on the skinny kernel for a 1280 x 1280 weight
-    # the batched decode step at M = 16: vocab (four-panel groups, tail panel),
+    # the batched decode step at M = 16: vocab (one panel per workgroup, tail panel),
     # q|k|v, FFN up and the 1280 x 1280 projections (single panels, unsplit)
     (16, 51866, 1280), (16, 3840, 1280), (16, 5120, 1280), (16, 1280, 1280),
 ])
