@@ -701,6 +701,7 @@ def staged_ok(c, x, qs, sc):
     (1, 3840, 1280), (2, 3840, 1280), (8, 5120, 1280), (16, 1280, 5120),
     (8, 51866, 1280),    # batched vocab logits, tail panel of 26 rows
     (24, 51866, 1280),   # vocab with 32-row slices: four panels per workgroup
+    (3, 51866, 1280), (13, 51866, 1280),  # vocab, 8- and 16-row tiles: rows past M
     (32, 1280, 1280), (33, 3840, 1280), (70, 1280, 5120), (5, 40, 64),
     (17, 5120, 1280),    # one 32-row slice, 15 rows past M
     (320, 640, 1280),    # ten slices (M = 320, the prefill's largest) of 20 panels
