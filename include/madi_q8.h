@@ -241,9 +241,18 @@ int madi_proj_f16w(float *out, const float *in, const void *w16, void *stage16, 
  * a write into or madi_free of the Q8 source, a partial overwrite of wdq; a
  * full overwrite or madi_free of wdq drops the record.  Kernels outside this
  * library that read wdq need madi_q8_materialize(wdq) first (NULL: every
- * record).  madi_set_deferred_dequant(0) materialises every record and makes
- * madi_q8_dequant_f16 write wdq at once (the default is 1). */
+ * record).  Code outside this library that WRITES into a recorded wdq or into
+ * its Q8 source (an engine kernel, hipMemcpy, a torch copy) calls
+ * madi_q8_forget(ptr, bytes) on the range first: a record whose wdq the range
+ * covers entirely is dropped, one whose wdq it covers in part or whose Q8
+ * source it touches is materialised (so wdq keeps the weights it was made
+ * from).  Without that call a later F16 GEMM on wdq would run the fused kernel
+ * on the recorded Q8 weight and a later materialisation would read the
+ * changed source.  madi_set_deferred_dequant(0) materialises every record and
+ * makes madi_q8_dequant_f16 write wdq at once (the default is 1).  No
+ * counterpart in the reference (Metal's kDeq writes wdq at once). */
 int madi_q8_materialize(void *wdq);
+int madi_q8_forget(void *ptr, size_t bytes);
 int madi_set_deferred_dequant(int on);
 
 /* ---- plain fp16 GEMMs (pre-dequantised F16 weights) ------------------------ */

@@ -6,6 +6,7 @@ travels with the source tree.  Run as `python -m madi_amd.build`.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import subprocess
 import sys
@@ -53,13 +54,16 @@ def build(verbose: bool = False, extra_flags=(), out: str = LIB, obj_dir: str = 
     """Compile all sources and link the library (default libmadi_q8.so next to
     this file); `extra_flags` (e.g. -D tuning macros) go to every compile."""
     os.makedirs(obj_dir, exist_ok=True)
-    objs = []
-    for src in sources():
-        obj = os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o")
-        msg = _run([HIPCC, *HIP_FLAGS, *extra_flags, "-c", src, "-o", obj])
-        if verbose and msg.strip():
-            print(msg)
-        objs.append(obj)
+    srcs = sources()
+    objs = [os.path.join(obj_dir, os.path.basename(src)[:-4] + ".o") for src in srcs]
+    # one hipcc per source, at most 8 at a time
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as pool:
+        msgs = list(pool.map(lambda so: _run([HIPCC, *HIP_FLAGS, *extra_flags, "-c", so[0], "-o", so[1]]),
+                             zip(srcs, objs)))
+    if verbose:
+        for msg in msgs:
+            if msg.strip():
+                print(msg)
     tmp = out + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs,
           "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"])

@@ -20,9 +20,10 @@
 // could observe wdq: a library op that reads it any other way, a download of
 // it, a write or free of the Q8 source, or an explicit madi_q8_materialize.  A
 // write into wdq (another dequant, an op's output, an upload) or its free
-// retires the record.  Reads of wdq by kernels outside this library are not
-// visible here: such a caller calls madi_q8_materialize first, or turns the
-// deferral off (madi_set_deferred_dequant(0)).
+// retires the record.  Reads and writes of wdq or of its Q8 source by code
+// outside this library are not visible here: such a caller calls
+// madi_q8_materialize before a read and madi_q8_forget before a write, or
+// turns the deferral off (madi_set_deferred_dequant(0)).
 #include <string.h>
 
 #include <vector>
@@ -206,6 +207,15 @@ extern "C" int madi_q8_materialize(void *wdq) {
   for (Deferred &d : g_def)
     if (d.wdq == reinterpret_cast<uintptr_t>(wdq)) return materialize(d);
   return MADI_OK;
+}
+
+extern "C" int madi_q8_forget(void *ptr, size_t bytes) {
+  if (!ptr || bytes == 0) return MADI_OK;
+  if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_forget: madi_init has not succeeded");
+  // the same bookkeeping as a write by this library: a recorded wdq that the
+  // write covers entirely is dropped, one it covers in part, or whose Q8
+  // source it touches, is written first
+  return deferred_before_write(ptr, bytes);
 }
 
 extern "C" int madi_set_deferred_dequant(int on) {

@@ -29,6 +29,12 @@ void f16gemm_cleanup();
 // the batched projection's many-row calls (gemm.hip); shapes checked by the caller.
 int q8_gemm_f32io(const float *in, const void *qs, const void *scales, float *out, uint32_t m,
                   uint32_t n, uint32_t k);
+// f16 rows through the batched projection kernel, f16 result (skinny.hip)
+int q8_skinny_f16io(const void *in, const void *qs, const void *scales, void *out, uint32_t m,
+                    uint32_t n, uint32_t k);
+bool skinny_f16_ok(const void *in, const void *qs, const void *out, uint32_t m, uint32_t n,
+                   uint32_t k);
+bool skinny_f16_prefers_gemm(uint32_t m, uint32_t n, uint32_t k);
 // Resolves the current device's address of the allocation-free GEMM's fixed
 // scratch array and clears its counters (madi_init).
 int gemm_scratch_init();

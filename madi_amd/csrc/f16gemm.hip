@@ -63,10 +63,14 @@ int gemm_f16_f32out(const char *what, const void *a, const void *b, float *c, ui
 }
 
 // The operands the fused Q8 GEMM needs (16-byte aligned A, C and bias, whole
-// 32-row panels); otherwise a recorded weight is materialised and the library
-// GEMM runs.
-inline bool fusable(const void *a, const void *c, const float *bias, uint32_t n) {
-  return aligned(a, 16) && aligned(c, 16) && (!bias || aligned(bias, 16)) && n % kPanelRows == 0;
+// 32-row panels, K a multiple of 64, and madi_q8_gemm's 32-bit buffer limits:
+// A, W and one 128-row C tile below 2 GiB); otherwise a recorded weight is
+// materialised and the library GEMM runs.
+inline bool fusable(const void *a, const void *c, const float *bias, uint32_t m, uint32_t n,
+                    uint32_t k) {
+  return aligned(a, 16) && aligned(c, 16) && (!bias || aligned(bias, 16)) && n % kPanelRows == 0 &&
+         k % kChunkK == 0 && (uint64_t)m * k * 2 < (1ull << 31) && (uint64_t)n * k < (1ull << 31) &&
+         (uint64_t)n * 256 < (1ull << 31);
 }
 
 // dst[i] = f16(src[i]) (round to nearest even), the engine's f32 -> f16 staging
@@ -113,7 +117,7 @@ extern "C" int madi_f16_gemm(const void *a, const void *b, void *c, const float 
   // GEMM runs on that weight (one rounding of acc + bias, the Q8-direct
   // kernel's epilogue, m4_gemm.metal:180-186) and b is never written
   const void *qs, *sc;
-  if (fusable(a, c, bias, n) && deferred_lookup(b, n, k, &qs, &sc))
+  if (fusable(a, c, bias, m, n, k) && deferred_lookup(b, n, k, &qs, &sc))
     return madi_q8_gemm(a, qs, sc, c, bias, m, n, k, epilogue);
   if (int rc = deferred_before_read(a, (size_t)m * k * 2)) return rc;
   if (int rc = deferred_before_read(b, (size_t)k * n * 2)) return rc;
@@ -139,10 +143,23 @@ extern "C" int madi_matmul_f16(const void *a, const void *b, void *c, int m, int
   if (!aligned(a, 2) || !aligned(b, 2) || !aligned(c, 2))
     return fail(MADI_ERR_ALIGN, "madi_matmul_f16: misaligned operand");
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_matmul_f16: madi_init has not succeeded");
+  // b is the F16 [K][N] copy deqW16 recorded for a Q8 weight [N][K]: the
+  // product runs from the Q8 weight and b is never written.  Few rows (the
+  // batched decode's logits, B = 8 or 16 over the vocab's 51866 rows,
+  // transcribe.zig:2391-2394) take the batched projection kernel, which
+  // handles any N; many rows on whole panels (the cross-attention K and V of
+  // the encoder output, transcribe.zig:2440-2448) the fused GEMM.
   const void *qs, *sc;
-  if (alpha == 1.0f && beta == 0.0f && fusable(a, c, nullptr, (uint32_t)n) &&
-      deferred_lookup(b, (uint32_t)n, (uint32_t)k, &qs, &sc))
-    return madi_q8_gemm(a, qs, sc, c, nullptr, (uint32_t)m, (uint32_t)n, (uint32_t)k, MADI_EPI_NONE);
+  const uint32_t um = (uint32_t)m, un = (uint32_t)n, uk = (uint32_t)k;
+  if (alpha == 1.0f && beta == 0.0f && deferred_lookup(b, un, uk, &qs, &sc)) {
+    if (skinny_f16_prefers_gemm(um, un, uk) && fusable(a, c, nullptr, um, un, uk))
+      return madi_q8_gemm(a, qs, sc, c, nullptr, um, un, uk, MADI_EPI_NONE);
+    if (skinny_f16_ok(a, qs, c, um, un, uk)) {
+      if (int rc = deferred_before_read(a, (size_t)um * uk * 2)) return rc;
+      if (int rc = deferred_before_write(c, (size_t)um * un * 2)) return rc;
+      return q8_skinny_f16io(a, qs, sc, c, um, un, uk);
+    }
+  }
   const size_t mn = (size_t)m * n * 2;
   if (int rc = deferred_before_read(a, (size_t)m * k * 2)) return rc;
   if (int rc = deferred_before_read(b, (size_t)k * n * 2)) return rc;

@@ -56,15 +56,20 @@ struct Plan {
 // panel, and XR/4 x 16 bytes of activations in a coalesced pattern: piece i
 // is row 4i + lane/16, floats 4 * (lane % 16) .. +3 of the chunk (each load
 // instruction reads four whole 256-byte row segments).
-template <int P, int XR>
+//
+// With f16 activations (H) the MFMA fragments come straight from memory: lane
+// (h, c) loads row c's 16 bytes of piece 4h + s for each k-step s (rows past
+// the slice's last row read zeros, outside the activation resource).
+template <int P, int XR, bool H = false>
 struct Chunk {
   u32x4 w[P][2];
   uint32_t s[P];
-  f32x4 x[XR / 4];
+  f32x4 x[H ? 1 : XR / 4];
+  u32x4 xh[H ? 4 : 1];
 };
 
-template <int P, int XR>
-__device__ inline void load_chunk(Chunk<P, XR> &b, const Plan<P> &pl, uint32_t c) {
+template <int P, int XR, bool H>
+__device__ inline void load_chunk(Chunk<P, XR, H> &b, const Plan<P> &pl, uint32_t c) {
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     const uint32_t so = (uint32_t)panel_chunk_qs(pl.K, pl.p[t], pl.R[t], c);
@@ -73,10 +78,16 @@ __device__ inline void load_chunk(Chunk<P, XR> &b, const Plan<P> &pl, uint32_t c
     b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(
         pl.ws, pl.s_voff[t], (uint32_t)panel_chunk_sc(pl.K, pl.p[t], pl.R[t], c) * 2, 0);
   }
+  if constexpr (H) {
 #pragma unroll
-  for (int i = 0; i < XR / 4; ++i)
-    b.x[i] = __builtin_bit_cast(
-        f32x4, __builtin_amdgcn_raw_buffer_load_b128(pl.xr, pl.x_voff + i * 16 * pl.K, c * kChunkK * 4, 0));
+    for (int s = 0; s < 4; ++s)
+      b.xh[s] = __builtin_amdgcn_raw_buffer_load_b128(pl.xr, pl.x_voff, c * kChunkK * 2 + s * 16, 0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < XR / 4; ++i)
+      b.x[i] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(pl.xr, pl.x_voff + i * 16 * pl.K, c * kChunkK * 4, 0));
+  }
 }
 
 // The wave's activation tile of one chunk in LDS: 32 rows x 64 f16, 128 bytes
@@ -89,21 +100,26 @@ __device__ inline uint32_t x_piece(uint32_t row, uint32_t j) {
 
 // acc[t] += W_t(chunk) . X(chunk)^T over the four k-steps; step s uses half
 // (s & 1) of weight unit s >> 1 and activation piece 4h + s of row c.
-template <int P, int XR>
-__device__ inline void accumulate(const Chunk<P, XR> &b, uint8_t *xt, uint32_t lane,
+template <int P, int XR, bool H>
+__device__ inline void accumulate(const Chunk<P, XR, H> &b, uint8_t *xt, uint32_t lane,
                                   f32x16 (&acc)[P]) {
   const uint32_t h = lane >> 5, c = lane & 31;
   // stage: f32 -> f16 (round to nearest even, the kCvt32 staging), 8 bytes per piece
+  if constexpr (!H) {
 #pragma unroll
-  for (int i = 0; i < XR / 4; ++i) {
-    const uint32_t row = 4 * i + (lane >> 4), k4 = lane & 15;  // floats 4*k4 .. +3
-    const f16x4 v = {(f16)b.x[i].x, (f16)b.x[i].y, (f16)b.x[i].z, (f16)b.x[i].w};
-    *reinterpret_cast<f16x4 *>(xt + x_piece(row, k4 >> 1) + (k4 & 1) * 8) = v;
+    for (int i = 0; i < XR / 4; ++i) {
+      const uint32_t row = 4 * i + (lane >> 4), k4 = lane & 15;  // floats 4*k4 .. +3
+      const f16x4 v = {(f16)b.x[i].x, (f16)b.x[i].y, (f16)b.x[i].z, (f16)b.x[i].w};
+      *reinterpret_cast<f16x4 *>(xt + x_piece(row, k4 >> 1) + (k4 & 1) * 8) = v;
+    }
   }
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
     f16x8 xf = {};
-    if (XR == 32 || c < XR) xf = *reinterpret_cast<const f16x8 *>(xt + x_piece(c, 4 * h + s));
+    if constexpr (H)
+      xf = __builtin_bit_cast(f16x8, b.xh[s]);
+    else if (XR == 32 || c < XR)
+      xf = *reinterpret_cast<const f16x8 *>(xt + x_piece(c, 4 * h + s));
 #pragma unroll
     for (int t = 0; t < P; ++t) {
       const f16x2 s2 = {__builtin_bit_cast(f16, (uint16_t)b.s[t]),
@@ -133,13 +149,14 @@ constexpr int skinny_lds() {
 // arguments are scalars in the order the kernel first needs them, so the
 // leading ones arrive preloaded in SGPRs, and the set-up has no integer
 // division: split s covers chunks [s * cper + min(s, crem), + cper + (s <
-// crem)).  `out`: f32 [m][n]; `ws`, `cnt`: partial tiles and arrival counters
+// crem)).  `x`, `out`: f32 [m][k], [m][n], or with H f16 [m][k], [m][n] (the
+// sum rounded once to f16); `ws`, `cnt`: partial tiles and arrival counters
 // (zero between uses) when K is split.
-template <int P, int KW, int XR, int WIN>
+template <int P, int KW, int XR, int WIN, bool H = false>
 __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 > 2 ? KW / 4 : 2))) void q8_skinny_kernel(
-    const uint8_t *__restrict__ qs, const f16 *__restrict__ sc, const float *__restrict__ x,
+    const uint8_t *__restrict__ qs, const f16 *__restrict__ sc, const void *__restrict__ x,
     uint32_t M, uint32_t N, uint32_t K, uint32_t cper, uint32_t crem, uint32_t groups,
-    float *__restrict__ out, f32x4 *ws, uint32_t *cnt) {
+    void *__restrict__ out, f32x4 *ws, uint32_t *cnt) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[skinny_lds<P, KW, XR>()];
 
   // Consecutive workgroups go to different XCDs (round-robin, x fastest).
@@ -177,14 +194,15 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 
   }
   const uint32_t m0 = slice * kSlice;
   const uint32_t rows = M - m0 < kSlice ? M - m0 : kSlice;
-  pl.xr = make_rsrc(x + (size_t)m0 * K, rows * K * 4);
-  pl.x_voff = (lane >> 4) * K * 4 + (lane & 15) * 16;
+  constexpr uint32_t xb = H ? 2 : 4;  // bytes per activation
+  pl.xr = make_rsrc(static_cast<const uint8_t *>(x) + (size_t)m0 * K * xb, rows * K * xb);
+  pl.x_voff = H ? r * K * 2 + h * 64 : (lane >> 4) * K * 4 + (lane & 15) * 16;
 
   uint8_t *xt = smem + wave * XR * 128;
-  Chunk<P, XR> win[WIN];
+  Chunk<P, XR, H> win[WIN];
 #pragma unroll
   for (int i = 0; i < WIN; ++i)
-    if (c0 + i < c1) load_chunk<P, XR>(win[i], pl, c0 + i);
+    if (c0 + i < c1) load_chunk<P, XR, H>(win[i], pl, c0 + i);
   f32x16 acc[P];
 #pragma unroll
   for (int t = 0; t < P; ++t) acc[t] = (f32x16){};
@@ -193,8 +211,8 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 
 #pragma unroll
     for (int i = 0; i < WIN; ++i) {
       if (c + i < c1) {
-        accumulate<P, XR>(win[i], xt, lane, acc);
-        if (c + i + WIN < c1) load_chunk<P, XR>(win[i], pl, c + i + WIN);
+        accumulate<P, XR, H>(win[i], xt, lane, acc);
+        if (c + i + WIN < c1) load_chunk<P, XR, H>(win[i], pl, c + i + WIN);
       }
     }
   }
@@ -262,7 +280,31 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 
   for (int t = 0; t < P; ++t) {
     if (grp * P + t >= np) break;
     const uint32_t R = pl.R[t];
-    float *o = out + (size_t)m * N + pl.p[t] * kPanelRows + nl;
+    if constexpr (H) {
+      f16 *o = static_cast<f16 *>(out) + (size_t)m * N + pl.p[t] * kPanelRows + nl;
+      const f16x4 hv = {(f16)v[t].x, (f16)v[t].y, (f16)v[t].z, (f16)v[t].w};
+      if (nl + 4 <= R) {
+        // o is 8-byte aligned when N % 4 == 0 and 4-byte aligned when N is
+        // even (out is 16-byte aligned and 32 p + nl is a multiple of 4)
+        if (N % 4 == 0) {
+          *reinterpret_cast<f16x4 *>(o) = hv;
+        } else if (N % 2 == 0) {
+          reinterpret_cast<f16x2 *>(o)[0] = (f16x2){hv.x, hv.y};
+          reinterpret_cast<f16x2 *>(o)[1] = (f16x2){hv.z, hv.w};
+        } else {
+          o[0] = hv.x;
+          o[1] = hv.y;
+          o[2] = hv.z;
+          o[3] = hv.w;
+        }
+      } else {
+        if (nl + 0 < R) o[0] = hv.x;
+        if (nl + 1 < R) o[1] = hv.y;
+        if (nl + 2 < R) o[2] = hv.z;
+      }
+      continue;
+    }
+    float *o = static_cast<float *>(out) + (size_t)m * N + pl.p[t] * kPanelRows + nl;
     if (nl + 4 <= R) {
       o[0] = v[t].x;
       o[1] = v[t].y;
@@ -292,16 +334,18 @@ constexpr int kVocabWaves = 4, kVocabWin = 2;
 constexpr int kGroupWaves = 4, kGroupWin = 2;
 constexpr uint32_t kMaxSplits = 4;
 
-// One projection: out[m][n] = sum_k x[m][k] w[n][k].
+// One projection: out[m][n] = sum_k x[m][k] w[n][k]; x and out f32, or f16
+// for the launches with H set.
 struct Proj {
-  float *out;
-  const float *x;
+  void *out;
+  const void *x;
   const uint8_t *qs;
   const f16 *sc;
   uint32_t m, n, k;
+  const char *what;
 };
 
-template <int P, int KW, int XR, int WIN>
+template <int P, int KW, int XR, int WIN, bool H = false>
 int launch_skinny(const Proj &a) {
   const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
   const uint32_t groups = (np + P - 1) / P, slices = (a.m + kSlice - 1) / kSlice;
@@ -319,22 +363,22 @@ int launch_skinny(const Proj &a) {
     ws = reinterpret_cast<f32x4 *>(w);
   }
   const dim3 grid((groups + 7) / 8 * 8, slices, splits);
-  hipLaunchKernelGGL((q8_skinny_kernel<P, KW, XR, WIN>), grid, dim3(KW * 64), 0, stream(), a.qs,
+  hipLaunchKernelGGL((q8_skinny_kernel<P, KW, XR, WIN, H>), grid, dim3(KW * 64), 0, stream(), a.qs,
                      a.sc, a.x, a.m, a.n, a.k, C / splits, C % splits, groups, a.out, ws, cnt);
-  return check_launch("madi_q8_pproj");
+  return check_launch(a.what);
 }
 
 // wide matrices (the vocab logits): one panel per workgroup up to 16 rows,
 // four panels sharing each activation load for 32-row slices; narrow ones
 // keep one panel per workgroup with eight waves
-template <int XR>
+template <int XR, bool H = false>
 int launch_rows(const Proj &a) {
   const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
   if (np >= 1024) {
-    if constexpr (XR <= 16) return launch_skinny<1, kVocabWaves, XR, kVocabWin>(a);
-    return launch_skinny<4, kGroupWaves, XR, kGroupWin>(a);
+    if constexpr (XR <= 16) return launch_skinny<1, kVocabWaves, XR, kVocabWin, H>(a);
+    return launch_skinny<4, kGroupWaves, XR, kGroupWin, H>(a);
   }
-  return launch_skinny<1, kPanelWaves, XR, kPanelWin>(a);
+  return launch_skinny<1, kPanelWaves, XR, kPanelWin, H>(a);
 }
 
 }  // namespace
@@ -378,9 +422,45 @@ extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const 
       aligned(out, 16) &&
       (uint64_t)m * k * 4 < (1ull << 31) && (uint64_t)n * 256 < (1ull << 31))
     return q8_gemm_f32io(in, qs, scales, out, m, n, k);
-  const Proj a{out, in, static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), m, n, k};
+  const Proj a{out, in, static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), m, n, k,
+               "madi_q8_pproj"};
   // a batch of up to 8 or 16 rows loads only those activation rows
   if (m <= 8) return launch_rows<8>(a);
   if (m <= 16) return launch_rows<16>(a);
   return launch_rows<32>(a);
 }
+
+namespace madi {
+// Rows from which an f16 projection on a recorded F16 copy runs the MFMA GEMM
+// (madi_q8_gemm) rather than this kernel: the batched projection's rule, for
+// weights whose rows fill whole 32-row panels.
+bool skinny_f16_prefers_gemm(uint32_t m, uint32_t n, uint32_t k) {
+  const uint64_t skinny_wgs = (uint64_t)((n + kPanelRows - 1) / kPanelRows) * ((m + kSlice - 1) / kSlice);
+  return n % kPanelRows == 0 && m >= kGemmRows &&
+         (n >= 2048 || k >= 4096 || skinny_wgs > (uint64_t)cu_count());
+}
+
+// out[M][N] (f16) = f16(in[M][K] (f16) . deq(W)^T), fp32 accumulation, any N
+// (the vocab's 51866 rows included): matmulF16Batched on a recorded F16 copy
+// of a Q8 weight (the batched decode's logits over deqW16's tok_emb copy,
+// engine/metal/transcribe.zig:2391-2394).  The caller checks the pointers and
+// the deferred state.
+int q8_skinny_f16io(const void *in, const void *qs, const void *scales, void *out, uint32_t m,
+                    uint32_t n, uint32_t k) {
+  const Proj a{out, in, static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), m, n, k,
+               "madi_matmul_f16"};
+  if (m <= 8) return launch_rows<8, true>(a);
+  if (m <= 16) return launch_rows<16, true>(a);
+  return launch_rows<32, true>(a);
+}
+
+// The f16 projection's limits: 32-bit buffer offsets (W and one 32-row slice
+// of activations below 2 GiB), 65535 slices, K % 64 == 0, 16-byte aligned
+// activations and output.
+bool skinny_f16_ok(const void *in, const void *qs, const void *out, uint32_t m, uint32_t n,
+                   uint32_t k) {
+  return k % kChunkK == 0 && (uint64_t)n * k < (1ull << 31) &&
+         (uint64_t)kSlice * k * 2 < (1ull << 31) && (m + kSlice - 1) / kSlice <= 65535 &&
+         aligned(in, 16) && aligned(qs, 16) && aligned(out, 16);
+}
+}  // namespace madi

@@ -64,6 +64,15 @@ def materialize(wdq=None) -> None:
     call("madi_q8_materialize", ptr(wdq))
 
 
+def forget(buf, nbytes: int | None = None) -> None:
+    """Announce a write by code outside the library (a torch copy, another
+    kernel) into [buf, buf + nbytes): records of deferred dequantisations
+    that the write would invalidate are dropped or materialised first."""
+    if nbytes is None:
+        nbytes = buf.numel() * buf.element_size()
+    call("madi_q8_forget", ptr(buf), nbytes)
+
+
 def set_deferred_dequant(on: bool) -> None:
     call("madi_set_deferred_dequant", 1 if on else 0)
 
@@ -274,7 +283,7 @@ def gemv_f16x(out, x16, w: Q8, n: int, k: int, bias=None, epilogue: int = EPI_NO
 
 __all__ = [
     "D", "MLP", "VOCAB", "ENC_SEQ", "NH", "Q8", "init", "sync", "getFunction", "materialize",
-    "set_deferred_dequant", "repack_host", "unpack_host",
+    "set_deferred_dequant", "forget", "repack_host", "unpack_host",
     "upload_q8", "upload_q8_device_repack", "quantize", "fnv", "FNV_SEED", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias", "kM4", "kM4Bias", "kFlash", "matmulF16Batched",
     "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "pproj", "proj", "kQkv", "kLogitGemv", "embLookup",
     "embLookupIndirect", "prefillEmbed", "gemv_f16x", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU",

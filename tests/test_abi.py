@@ -105,6 +105,9 @@ def test_function_handles_by_name():
     ("madi_flash_enc_f16", (FAKE, FAKE + 0x1000000, FAKE + 0x100000, FAKE + 0x3000000, 1500, 20), -9),  # out over k
     ("madi_flash_enc_f16", (FAKE, FAKE + 0x100, FAKE + 0x2000000, FAKE + 0x3000000, 1500, 20), -9),  # out over q
     ("madi_flash_enc_f16", (FAKE, FAKE, FAKE + 0x2000000, FAKE + 0x3000000, 1500, 20), -8),  # in place on q
+    ("madi_q8_forget", (FAKE, 4096), -8),
+    ("madi_matmul_f16", (FAKE, FAKE, FAKE, 0, 51866, 1280, 1.0, 0.0), -5),
+    ("madi_matmul_f16", (FAKE, FAKE, FAKE, 8, 51866, 1280, 1.0, 0.0), -8),
     ("madi_alloc", (16,), None),
     ("madi_sync", (), -8),
     ("madi_upload", (FAKE, FAKE, 16), -8),

@@ -294,3 +294,156 @@ def test_deferred_dequant_is_written_when_observable(q):
     assert normwise(host_f16(c), ref) <= TOL
     for b in (wdq, bq, bs):
         b.free()
+
+
+VOCAB = 51866
+
+
+@pytest.fixture(scope="module")
+def tok_emb(q):
+    """The tied token embedding as a Q8 weight [VOCAB][D] (seeded, synthetic)."""
+    rng = np.random.default_rng(2391)
+    qs, sc = synth.q8_weight(rng, VOCAB, D)
+    return qs, sc, q.upload_q8(qs, sc)
+
+
+def test_batched_logits_unchanged_sequence(q, tok_emb):
+    """The batched decode's logit step exactly as transcribe.zig:1358 and
+    2391-2394 issue it: deqW16 of the tied tok_emb into bb_temb once, then per
+    step kCvt32 (f32 -> f16 rows), matmulF16Batched(bb_x16, bb_temb, bb_l16,
+    B, VOCAB, D) and kCvt16.  The two conversions are engine kernels outside
+    this path (torch casts here).  bb_temb is never written (the product ran
+    from the Q8 weight, 51866 rows with a 26-row last panel); the f16 logits
+    equal the batched projection's f32 sums rounded once to f16, bit for bit
+    (same kernel, same accumulation order), and match the oracle."""
+    qs, sc, w = tok_emb
+    bb_temb = sentinel(D * VOCAB)
+    q.deqW16(bb_temb, w, VOCAB, D)
+    rng = np.random.default_rng(2393)
+    for B in (8, 16, 3):
+        say(f"batched logits B={B}")
+        xb = rng.standard_normal((B, D)).astype(np.float32)
+        bb_x16 = dev(xb).half().view(torch.int16)                        # kCvt32
+        bb_l16 = sentinel(B * VOCAB)
+        q.matmulF16Batched(bb_x16, bb_temb, bb_l16, B, VOCAB, D)
+        logits = bb_l16.view(torch.float16).float()                      # kCvt16
+        want = torch.empty((B, VOCAB), dtype=torch.float32, device="cuda")
+        q.pproj(bb_x16.view(torch.float16).float(), w, want, B, VOCAB, D)
+        q.sync()
+        assert torch.equal(bb_l16.view(torch.float16).view(B, VOCAB), want.half()), B
+        x16 = host_f16(bb_x16).reshape(B, D)
+        ref = O.q8_gemm_rows(x16, qs, sc, threads=16)
+        got = logits.cpu().numpy().reshape(B, VOCAB)
+        assert np.all(np.isfinite(got))
+        assert normwise(got, ref) <= TOL, B
+    assert np.all(bb_temb.cpu().numpy().view(np.uint16) == NAN16)
+
+
+def test_cross_kv_unchanged_sequence(q):
+    """The per-slot cross-attention K/V build exactly as transcribe.zig:
+    2440-2448 issues it: per layer deqW16(cross_wdq, ckw) then
+    matmulF16Batched(eo16, cross_wdq, ckc, actx, D, D), and the same for V
+    (biasAdd16 after it is an engine kernel outside this path).  actx is the
+    full window (1500 rows, fused GEMM), a shrunk audio context (750, fused
+    GEMM) and a short one (100, the batched projection kernel).  cross_wdq is
+    never written; K and V match the oracle; rows past actx of the ENC_SEQ-row
+    caches are untouched."""
+    rng = np.random.default_rng(2440)
+    ckq, cks = synth.q8_weight(rng, D, D)
+    cvq, cvs = synth.q8_weight(rng, D, D)
+    ckw, cvw = q.upload_q8(ckq, cks), q.upload_q8(cvq, cvs)
+    eo = synth.activations(rng, M, D)
+    eo16 = dev_f16(eo)
+    cross_wdq = sentinel(D * D)
+    for actx in (1500, 750, 100):
+        say(f"cross K/V actx={actx}")
+        ckc, cvc = sentinel(M * D), sentinel(M * D)
+        q.deqW16(cross_wdq, ckw, D, D)
+        q.matmulF16Batched(eo16, cross_wdq, ckc, actx, D, D)
+        q.deqW16(cross_wdq, cvw, D, D)
+        q.matmulF16Batched(eo16, cross_wdq, cvc, actx, D, D)
+        q.sync()
+        assert np.all(cross_wdq.cpu().numpy().view(np.uint16) == NAN16)
+        rows = ROWS[ROWS < actx]
+        for cache, wq, ws in ((ckc, ckq, cks), (cvc, cvq, cvs)):
+            h = cache.cpu().numpy().view(np.uint16).reshape(M, D)
+            assert np.all(h[actx:] == NAN16), actx
+            got = h[rows].view(np.float16).astype(np.float64)
+            assert np.all(np.isfinite(got))
+            ref = O.q8_gemm_rows(eo[:actx], wq, ws, rows=rows, threads=16)
+            assert normwise(got, ref) <= TOL, actx
+
+
+def test_matmul_f16_recorded_any_width(q):
+    """matmulF16Batched on a recorded copy whose width is not a multiple of 32
+    or even of 2 (97 and 1002 rows: partial last panels, 2- and 4-byte aligned
+    output rows) runs the batched projection kernel; alpha / beta other than
+    (1, 0) materialise the copy and run the library GEMM on it."""
+    rng = np.random.default_rng(4242)
+    k = 256
+    for n, m in ((97, 5), (1002, 24), (97, 40)):
+        say(f"recorded copy n={n} m={m}")
+        qs, sc = synth.q8_weight(rng, n, k)
+        w = q.upload_q8(qs, sc)
+        wdq = sentinel(k * n)
+        q.deqW16(wdq, w, n, k)
+        a = synth.activations(rng, m, k)
+        c = sentinel(m * n)
+        q.matmulF16Batched(dev_f16(a), wdq, c, m, n, k)
+        q.sync()
+        assert np.all(wdq.cpu().numpy().view(np.uint16) == NAN16)
+        got = host_f16(c).reshape(m, n).astype(np.float64)
+        assert normwise(got, O.q8_gemm_rows(a, qs, sc)) <= TOL
+        # alpha = 0.5: the library GEMM on the materialised copy
+        c2 = sentinel(m * n)
+        q.matmulF16Batched(dev_f16(a), wdq, c2, m, n, k, alpha=0.5)
+        q.sync()
+        assert np.array_equal(wdq.cpu().numpy().view(np.uint16),
+                              O.dequant_q8_f16(qs, sc).view(np.uint16).reshape(-1))
+        got2 = host_f16(c2).reshape(m, n).astype(np.float64)
+        assert normwise(got2, 0.5 * O.q8_gemm_rows(a, qs, sc)) <= TOL
+
+
+def test_outside_writes_announced_with_forget(q):
+    """Writes by code outside the library (torch copies here) into a recorded
+    wdq or its Q8 source, announced with madi_q8_forget: a full overwrite of
+    wdq drops the record (the next F16 GEMM multiplies the new data), a
+    partial one lands on top of the dequantised weights, and a write into the
+    Q8 source leaves wdq with the weights it was recorded from."""
+    say("outside writes and madi_q8_forget")
+    rng = np.random.default_rng(4388)
+    n, k, m = 128, 256, 40
+    qs, sc = synth.q8_weight(rng, n, k)
+    want = O.dequant_q8_f16(qs, sc).view(np.uint16).reshape(-1)
+    w = q.upload_q8(qs, sc)
+    a = synth.activations(rng, m, k)
+    # 1. full overwrite of wdq from torch
+    wdq = sentinel(k * n)
+    q.kDeq(wdq, w, n, k)
+    w16 = (rng.standard_normal((k, n)) * 0.01).astype(np.float16)
+    q.forget(wdq)
+    wdq.copy_(dev_f16(w16).view(-1))
+    c = torch.empty((m, n), dtype=torch.int16, device="cuda")
+    q.kM4("m4_gemm_nn", dev_f16(a), wdq, c, m, n, k)
+    q.sync()
+    ref = a.astype(np.float64) @ w16.astype(np.float64)
+    assert normwise(host_f16(c), ref) <= TOL
+    # 2. partial overwrite: the untouched part holds the dequantised weights
+    wdq = sentinel(k * n)
+    q.kDeq(wdq, w, n, k)
+    head = wdq[:64]
+    q.forget(head)
+    head.copy_(torch.arange(64, dtype=torch.int16, device="cuda"))
+    q.sync()
+    got = wdq.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got[:64], np.arange(64, dtype=np.uint16))
+    assert np.array_equal(got[64:], want[64:])
+    # 3. a write into the Q8 source: wdq keeps the recorded weights
+    wdq = sentinel(k * n)
+    src = q.upload_q8(qs, sc)
+    q.kDeq(wdq, src, n, k)
+    qt = src._keep[0]
+    q.forget(qt)
+    qt.zero_()
+    q.sync()
+    assert np.array_equal(wdq.cpu().numpy().view(np.uint16), want)

@@ -82,11 +82,14 @@ def test_noalloc_rejects_bad_arguments(q):
 
 def test_noalloc_under_graph_capture(q):
     """A fresh library (its growable workspace back at the 4 MiB of madi_init)
-    captures the fc2 + bias GEMM at M = 1500, whose 15 MiB of split-K partials
-    madi_q8_gemm could only get by growing the workspace, which capture
-    forbids; the allocation-free entry point needs no buffer.  Every replay,
-    with eager work between them, equals the eager result."""
-    m, n, k = 1500, 1280, 5120
+    captures 1000 x 5120 -> 1280 + bias: 80 tiles of 64 x 256 with K split
+    three ways across workgroups, whose 15.7 MB of fp32 partial tiles and
+    arrival counters live in the library's fixed scratch array.  Inside the
+    capture, madi_q8_gemm on the same shape is refused (its workspace would
+    have to grow, which capture forbids; nothing is launched), so the capture
+    needs the allocation-free route.  Every replay, with eager split-K calls
+    on the same scratch between them, equals the eager result."""
+    m, n, k = 1000, 1280, 5120
     say(f"noalloc graph capture m={m} n={n} k={k}")
     _lib.lib().madi_cleanup()
     q.init()
@@ -99,21 +102,30 @@ def test_noalloc_under_graph_capture(q):
     g = torch.cuda.CUDAGraph()
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
+    refused = None
     with torch.cuda.stream(side):
         with torch.cuda.graph(g, stream=side):
             q.init(side)
+            refused = _lib.lib().madi_q8_gemm(a_d.data_ptr(), w.qs, w.scales, c.data_ptr(),
+                                              b_d.data_ptr(), m, n, k, _lib.EPI_BIAS)
             _lib.call("madi_q8_gemm_noalloc", a_d.data_ptr(), w.qs, w.scales, c.data_ptr(),
                       b_d.data_ptr(), m, n, k, _lib.EPI_BIAS)
     q.init()
+    assert refused == -9, refused  # MADI_ERR_ARG: the workspace cannot grow under capture
     want = run(q, "madi_q8_gemm", a_d, w, b_d, m, n, k, _lib.EPI_BIAS)
     for rep in range(3):
         c.fill_(-1)
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(c.cpu().numpy(), want), rep
-        # eager work between replays: a smaller split shape on the same scratch
+        # eager work between replays: smaller split shapes through the same
+        # scratch (257 rows: four splits over 25 tiles) and the workspace
         a2, qs2, sc2 = synth.gemm_case(57 + rep, 257, 1280, 5120)
         w2 = q.upload_q8(qs2, sc2)
         a2_d = dev_f16(a2)
         assert np.array_equal(run(q, "madi_q8_gemm_noalloc", a2_d, w2, None, 257, 1280, 5120, 0),
                               run(q, "madi_q8_gemm", a2_d, w2, None, 257, 1280, 5120, 0))
+    rows = np.unique(np.r_[0, 63, 64, 500, m - 1])
+    ref = O.q8_gemm_rows(a, qs, sc, rows=rows, bias=bias, epilogue=_lib.EPI_BIAS, threads=8)
+    got = want.view(np.float16)[rows].astype(np.float64)
+    assert np.max(np.abs(got - ref)) / np.max(np.abs(ref)) <= 1e-3
