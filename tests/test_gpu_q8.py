@@ -292,10 +292,11 @@ def test_gemm_bias_epilogues(q, gelu, m, n):
 
 
 # Every encoder and cross-attention projection at M = 1500 (one 30 s window)
-# and the kernel instance it runs on a 256-CU device: fc1 128-row tiles (240),
-# q|k|v 96-row tiles (240), cross K|V 64-row tiles (240), out-proj 32-row
-# tiles (235), fc2 64-row tiles (120) x 2 K splits of 40 chunks; all K loops
-# unpadded (20 or 40 chunks per workgroup).
+# and the kernel instance it runs on a 256-CU device: fc1 128 x 256 tiles
+# (240), q|k|v 96 x 256 tiles (240), cross K|V 128 x 128 tiles (240), out-proj
+# 64 x 128 tiles (240), all with unpadded 20-chunk K loops; fc2 128 x 64 tiles
+# (240) with K split four ways inside the workgroup (q8_gemm_ks_kernel, 20
+# chunks per wave, the partials meeting in LDS).
 ENCODER_SHAPES = [("fc1", 5120, 1280), ("fc2", 1280, 5120), ("qkv", 3840, 1280),
                   ("out", 1280, 1280), ("cross_kv", 2560, 1280)]
 
@@ -319,16 +320,20 @@ def test_gemm_encoder_shapes_full_m(q, name, n, k):
                                            ("qkv", 3840, 1280, False), ("out", 1280, 1280, False)])
 def test_gemm_encoder_epilogues_full_m(q, name, n, k, gelu):
     """The encoder's production epilogue instances at M = 1500: fc1 + bias +
-    GELU on 128-row tiles with an unpadded 20-chunk loop, fc2 + bias where the
-    two K splits meet in the last workgroup before the bias, q|k|v + bias on
-    96-row and out + bias on 32-row tiles (encoder.zig:262-301)."""
+    GELU on 128 x 256 tiles with an unpadded 20-chunk loop, fc2 + bias where
+    the four in-workgroup K ranges meet in LDS before the bias, q|k|v + bias
+    on 96 x 256 and out + bias on 64 x 128 tiles (encoder.zig:262-301)."""
     say(f"gemm encoder epilogue {name} m=1500 n={n} k={k} gelu={gelu}")
     m = 1500
     a, qs, sc = synth.gemm_case(5, m, n, k)
     bias = np.random.default_rng(n + k).standard_normal(n).astype(np.float32)
     ref_rows = np.unique(np.r_[tile_rows(m), 1, 129, 1498])
-    for rep in range(2 if name == "fc2" else 1):  # split K: the counters must return to zero
+    first = None
+    for rep in range(2 if name == "fc2" else 1):  # split K: a rerun gives the same bits
         c = _gemm(q, a, qs, sc, bias=bias, gelu=gelu)
+        if first is None:
+            first = c.copy()
+        assert np.array_equal(c.view(np.uint16), first.view(np.uint16)), rep
         ref = O.q8_gemm_rows(a, qs, sc, rows=ref_rows, bias=bias,
                              epilogue=O.EPI_BIAS_GELU if gelu else O.EPI_BIAS, threads=16)
         assert normwise(c[ref_rows], ref) <= TOL, rep
@@ -535,10 +540,11 @@ def test_gemv_zero_blocks_are_exact(q, x_f16):
 @pytest.mark.parametrize("case", ["full_mantissa", "huge", "tiny", "mixed_in_block", "zero_blocks"])
 def test_gemv_f32_activations(q, case):
     """f32 activations with full 24-bit mantissas and wide ranges: the kernel
-    splits each 32-element block, scaled by a power of two, into f16 high and
-    low halves, so every product keeps ~22 bits.  Bar per row: the float64
-    sum within (K 2^-24 + 2^-21) sum_k |x_k q_k s_k| (f32 accumulation plus
-    the split), far below what a lost scale factor or a dropped half makes."""
+    multiplies each f32 x by the exact integer q in fp32 FMAs, one partial sum
+    per 32-element block, then scales the partial by the block's scale.  Bar
+    per row: the float64 sum within (K 2^-24 + 2^-21) sum_k |x_k q_k s_k|
+    (fp32 accumulation), far below what a lost scale factor or a dropped
+    block makes."""
     n, k = 256, 1280
     rng = np.random.default_rng(7 * len(case) + ord(case[0]))
     qs, sc = synth.q8_weight(rng, n, k)
