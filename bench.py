@@ -160,6 +160,19 @@ def _timed(torch, stream, fn, reps):
     return e0.elapsed_time(e1) * 1e-3 / reps
 
 
+def _timed_list(torch, stream, lst, reps, per=1):
+    """Average seconds per `per` calls' worth of lst (an IssueList replayed from
+    C) over `reps` back-to-back replays, after min(reps, 4) untimed ones."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    lst.run(min(reps, 4))
+    torch.cuda.synchronize()
+    e0.record(stream)
+    lst.run(reps)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e-3 / (reps * per)
+
+
 def _upload_layer(q8, seed, n, k):
     from madi_amd import synth
     qs, sc = synth.q8_weight(np.random.default_rng(seed), n, k)
@@ -170,8 +183,9 @@ def config_encoder_window(torch, stream, q8, reps=3):
     """The encoder GEMM set of one 30 s window: 32 layers x (q|k|v stacked
     1280->3840, out 1280->1280, fc1 1280->5120 + bias + GELU, fc2 5120->1280 +
     bias) at M = 1500, independent seeded weights per layer (668 MB, so every
-    layer's weights stream from HBM)."""
+    layer's weights stream from HBM).  Issued from C (madi_amd.issue)."""
     from madi_amd import synth
+    from madi_amd.issue import IssueList
     m = 1500
     a = torch.from_numpy(synth.activations(np.random.default_rng(100), m, 5120).view(np.int16)).cuda()
     c = torch.empty((m, 5120), dtype=torch.int16, device="cuda")
@@ -179,37 +193,89 @@ def config_encoder_window(torch, stream, q8, reps=3):
     layers = [[_upload_layer(q8, 1000 + 4 * l + j, n, k) for j, (_, n, k) in enumerate(ENC_SHAPES)]
               for l in range(ENC_LAYERS)]
     torch.cuda.synchronize()
-
-    def window(_):
-        for ws in layers:
-            q8.kGemmQ8(a, ws[0], c, m, 3840, 1280)
-            q8.kGemmQ8(a, ws[1], c, m, 1280, 1280)
-            q8.kGemmQ8Bias(a, ws[2], c, bias, m, 5120, 1280, gelu=True)
-            q8.kGemmQ8Bias(a, ws[3], c, bias, m, 1280, 5120)
-
-    window(0)
-    t = _timed(torch, stream, window, reps)
+    EPI = {0: (None, q8.EPI_NONE), 1: (None, q8.EPI_NONE), 2: (bias, q8.EPI_BIAS_GELU),
+           3: (bias, q8.EPI_BIAS)}
+    window = IssueList()
+    for ws in layers:
+        for j, (_, n, k) in enumerate(ENC_SHAPES):
+            window.kGemmQ8(a, ws[j], c, m, n, k, *EPI[j])
+    t = _timed_list(torch, stream, window, reps)
     flops = ENC_LAYERS * sum(2.0 * m * n * k for _, n, k in ENC_SHAPES)
     per = {}
     for j, (name, n, k) in enumerate(ENC_SHAPES):
-        def one(i, j=j, n=n, k=k):
-            ws = layers[i % ENC_LAYERS][j]
-            if j == 2:
-                q8.kGemmQ8Bias(a, ws, c, bias, m, n, k, gelu=True)
-            elif j == 3:
-                q8.kGemmQ8Bias(a, ws, c, bias, m, n, k)
-            else:
-                q8.kGemmQ8(a, ws, c, m, n, k)
-        tj = _timed(torch, stream, one, ENC_LAYERS)
+        one = IssueList()
+        for ws in layers:
+            one.kGemmQ8(a, ws[j], c, m, n, k, *EPI[j])
+        tj = _timed_list(torch, stream, one, 2, per=ENC_LAYERS)
         per[name] = {"us": round(tj * 1e6, 2), "tflops": round(2.0 * m * n * k / tj / 1e12, 1)}
     del layers
     return {
         "workload": "32 layers x (qkv 1280->3840, out 1280->1280, fc1 1280->5120 +bias+GELU, "
-                    "fc2 5120->1280 +bias) Q8 GEMMs at M=1500, independent weights per layer",
+                    "fc2 5120->1280 +bias) Q8 GEMMs at M=1500, independent weights per layer, "
+                    "issued from C",
         "ms_per_window": round(t * 1e3, 4), "tflop_per_window": round(flops / 1e12, 4),
         "tflops": round(flops / t / 1e12, 1),
         "frac_fp16_peak": round(flops / t / 1e12 / PEAK_FP16_TFLOPS, 4),
         "per_gemm_cold": per,
+    }
+
+
+def config_encoder_window_engine(torch, stream, q8, reps=3):
+    """The encoder's Q8 GEMMs of one 30 s window exactly as encoder.zig:256-303
+    issues them on its tensor-op path: per layer kDeq of each Q8 weight into the
+    F16 scratch (s.wdq / s.wdq2) and kM4 / kM4Bias through the handles of
+    m4_gemm_bias, m4_gemm_nn and m4_gemm_bias_gelu: q, k and v as three
+    1280->1280 GEMMs + bias from row slices of the stacked q|k|v weight into
+    the three blocks of s.qkv, out-proj 1280->1280 without bias, fc1
+    1280->5120 + bias + GELU, fc2 5120->1280 without bias (its bias goes into
+    the next layer norm).  32 layers, independent weights, M = 1500, issued
+    from C through the boundary (madi_m4_gemm on the recorded scratch)."""
+    from madi_amd import synth
+    from madi_amd.issue import IssueList
+    m, d, mlp = 1500, DIM, 5120
+    rng = np.random.default_rng(110)
+    f16 = lambda r, c_: torch.from_numpy(synth.activations(rng, r, c_).view(np.int16)).cuda()
+    f32 = lambda n: torch.from_numpy(rng.standard_normal(n).astype(np.float32)).cuda()
+    x_ln, ao, x_ln2 = f16(m, d), f16(m, d), f16(m, d)
+    qkv = torch.empty((3, m, d), dtype=torch.int16, device="cuda")   # s.qkv: q | k | v blocks
+    mo = torch.empty((m, d), dtype=torch.int16, device="cuda")
+    mh = torch.empty((m, mlp), dtype=torch.int16, device="cuda")
+    wdq = torch.empty(d * mlp, dtype=torch.int16, device="cuda")     # Scratch.wdq
+    wdq2 = torch.empty(d * mlp, dtype=torch.int16, device="cuda")    # Scratch.wdq2
+    m4, m4b, m4bg = (q8.getFunction(nm) for nm in ("m4_gemm_nn", "m4_gemm_bias", "m4_gemm_bias_gelu"))
+    layers = []
+    for l in range(ENC_LAYERS):
+        layers.append(dict(
+            qkv=_upload_layer(q8, 6000 + 8 * l, 3 * d, d), o=_upload_layer(q8, 6001 + 8 * l, d, d),
+            m0=_upload_layer(q8, 6002 + 8 * l, mlp, d), m2=_upload_layer(q8, 6003 + 8 * l, d, mlp),
+            qb=f32(d), kb=f32(d), vb=f32(d), m0b=f32(mlp)))
+    torch.cuda.synchronize()
+    q_, k_, v_ = (qkv[i] for i in range(3))
+    window = IssueList()
+    for L in layers:
+        window.kDeq(wdq, L["qkv"], d, d)
+        window.kM4Bias(m4b, x_ln, wdq, q_, L["qb"], m, d, d)
+        window.kDeq(wdq2, L["qkv"].rows(d, d), d, d)
+        window.kM4Bias(m4b, x_ln, wdq2, k_, L["kb"], m, d, d)
+        window.kDeq(wdq, L["qkv"].rows(2 * d, d), d, d)
+        window.kM4Bias(m4b, x_ln, wdq, v_, L["vb"], m, d, d)
+        window.kDeq(wdq, L["o"], d, d)
+        window.kM4(m4, ao, wdq, mo, m, d, d)
+        window.kDeq(wdq, L["m0"], mlp, d)
+        window.kM4Bias(m4bg, x_ln2, wdq, mh, L["m0b"], m, mlp, d)
+        window.kDeq(wdq2, L["m2"], d, mlp)
+        window.kM4(m4, mh, wdq2, mo, m, d, mlp)
+    t = _timed_list(torch, stream, window, reps)
+    flops = ENC_LAYERS * 2.0 * m * (4 * d * d + 2 * d * mlp)
+    del layers
+    return {
+        "workload": "32 layers x (q, k, v 1280->1280 +bias from slices of the stacked weight, "
+                    "out 1280->1280, fc1 1280->5120 +bias+GELU, fc2 5120->1280) at M=1500 as "
+                    "encoder.zig:256-303 issues them (kDeq + kM4/kM4Bias handles through the "
+                    "deferred dequantisation), independent weights per layer, issued from C",
+        "ms_per_window": round(t * 1e3, 4), "tflop_per_window": round(flops / 1e12, 4),
+        "tflops": round(flops / t / 1e12, 1),
+        "frac_fp16_peak": round(flops / t / 1e12 / PEAK_FP16_TFLOPS, 4),
     }
 
 
@@ -234,20 +300,28 @@ def config_batched_decode(torch, stream, q8, reps=20):
                        "cross out 1280->1280, ffn 1280->5120->1280) + vocab 1280->51866, skinny "
                        "Q8 projection, weights cold (two alternating sets)",
            "weight_bytes_per_step": step_bytes}
+    from madi_amd.issue import IssueList
     for m in (8, 16):
-        def step(i, m=m):
+        def step(i, m=m, lst=None):
             layers, vocab = sets[i % 2]
+            q = lst if lst is not None else q8
             for ws in layers:
                 for j, (_, n, k) in enumerate(DEC_SHAPES):
-                    q8.pproj(xin, ws[j], out, m, n, k)
-            q8.pproj(xin, vocab, out, m, VOCAB, DIM)
+                    q.pproj(xin, ws[j], out, m, n, k)
+            q.pproj(xin, vocab, out, m, VOCAB, DIM)
         step(0)
         step(1)
-        t = _timed(torch, stream, step, reps)
+        tp = _timed(torch, stream, step, reps)
+        two = IssueList()   # two steps, one per weight set
+        step(0, lst=two)
+        step(1, lst=two)
+        t = _timed_list(torch, stream, two, reps // 2, per=2)
         byts = step_bytes + DEC_LAYERS * sum(m * k * 4 + m * n * 4 for _, n, k in DEC_SHAPES) \
             + m * DIM * 4 + m * VOCAB * 4
         res[f"m{m}"] = {"us_per_step": round(t * 1e6, 2), "gbs": round(byts / t / 1e9, 1),
-                        "frac_hbm_peak": round(byts / t / 1e9 / PEAK_HBM_GBS, 4)}
+                        "frac_hbm_peak": round(byts / t / 1e9 / PEAK_HBM_GBS, 4),
+                        "issued_from": "C (madi_amd.issue)",
+                        "python_issued_us_per_step": round(tp * 1e6, 2)}
         tv = _timed(torch, stream, lambda i, m=m: q8.pproj(xin, sets[i % 2][1], out, m, VOCAB, DIM),
                     reps)
         vb = VOCAB * DIM + VOCAB * (DIM // 32) * 2 + m * DIM * 4 + m * VOCAB * 4
@@ -294,27 +368,35 @@ def config_decode_token(torch, stream, q8, reps=20):
     f_gelu = q8.getFunction("gemv_q8_bias_gelu")  # the handles decoder.zig resolves once
     f_res = q8.getFunction("gemv_q8_bias_res")
 
-    def token(i):
+    def token(i, lst=None):
         layers, vocab = sets[i % 2]
+        q_ = lst if lst is not None else q8
         for w in layers:
-            q8.kQkv(q, xb, w[0], qb, vb, kc, vc, pos, d)
-            q8.kGemvQ8(mo, ao, w[1], d, d)
-            q8.kGemvQ8Bias(q, xb, w[2], bd, d, d)
-            q8.kGemvQ8(mo, ao, w[3], d, d)
-            q8.kGemvQ8BiasEpi(f_gelu, mh, xb, w[4], bm, mlp, d)
-            q8.kGemvQ8BiasEpi(f_res, x, mh, w[5], bd, d, mlp)
-        q8.kLogitGemv(logits, vocab.qs, vocab.scales, xb, VOCAB, DIM)
+            q_.kQkv(q, xb, w[0], qb, vb, kc, vc, pos, d)
+            q_.kGemvQ8(mo, ao, w[1], d, d)
+            q_.kGemvQ8Bias(q, xb, w[2], bd, d, d)
+            q_.kGemvQ8(mo, ao, w[3], d, d)
+            q_.kGemvQ8BiasEpi(f_gelu, mh, xb, w[4], bm, mlp, d)
+            q_.kGemvQ8BiasEpi(f_res, x, mh, w[5], bd, d, mlp)
+        q_.kLogitGemv(logits, vocab.qs, vocab.scales, xb, VOCAB, DIM)
 
+    from madi_amd.issue import IssueList
     token(0)
     token(1)
-    t = _timed(torch, stream, token, reps)
+    tp = _timed(torch, stream, token, reps)
+    two = IssueList()   # two tokens, one per weight set
+    token(0, two)
+    token(1, two)
+    t = _timed_list(torch, stream, two, reps // 2, per=2)
     res = {"workload": "decoder token at M = 1: 4 layers x (q|k|v + K/V store 1280->3840, out, "
                        "cross-q + bias, cross-out 1280->1280, FFN-up + bias + GELU 1280->5120, "
                        "FFN-down + bias + residual 5120->1280) + vocab logits 1280->51866, GEMV "
                        "family, f32 activations, weights cold (two alternating sets)",
            "weight_bytes_per_token": step_bytes,
            "us_per_token": round(t * 1e6, 2), "gbs": round(step_bytes / t / 1e9, 1),
-           "frac_hbm_peak": round(step_bytes / t / 1e9 / PEAK_HBM_GBS, 4)}
+           "frac_hbm_peak": round(step_bytes / t / 1e9 / PEAK_HBM_GBS, 4),
+           "issued_from": "C (madi_amd.issue)",
+           "python_issued_us_per_token": round(tp * 1e6, 2)}
     del sets
     base = _upload_layer(q8, 4990, 3 * d, d)
     ws = []
@@ -372,13 +454,28 @@ def config_long_audio(torch, stream, q8, reps=5):
     c = torch.empty((m, 5120), dtype=torch.int16, device="cuda")
     res = {"workload": "fc1 M=24000 K=1280 N=5120, fc2 M=24000 K=5120 N=1280 Q8 GEMMs "
                        "(activations drawn on the device: torch Philox N(0,1) -> f16)"}
+    res["clocks"] = ("first: one launch after 0.2 s idle (the clock the chip starts a "
+                     "window at); sustained: the average of 5 launches after 8 untimed ones "
+                     "back to back (the clock it settles to under continuous MFMA load)")
     for name, n, k in (("fc1", 5120, 1280), ("fc2", 1280, 5120)):
         w = _upload_layer(q8, 3000 + n, n, k)
         q8.kGemmQ8(a, w, c, m, n, k)
+        torch.cuda.synchronize()
+        time.sleep(0.2)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        q8.kGemmQ8(a, w, c, m, n, k)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t1 = e0.elapsed_time(e1) * 1e-3
+        for _ in range(8):
+            q8.kGemmQ8(a, w, c, m, n, k)
         t = _timed(torch, stream, lambda i: q8.kGemmQ8(a, w, c, m, n, k), reps)
         fl = 2.0 * m * n * k
         res[name] = {"us": round(t * 1e6, 1), "tflops": round(fl / t / 1e12, 1),
-                     "frac_fp16_peak": round(fl / t / 1e12 / PEAK_FP16_TFLOPS, 4)}
+                     "frac_fp16_peak": round(fl / t / 1e12 / PEAK_FP16_TFLOPS, 4),
+                     "first_launch_us": round(t1 * 1e6, 1),
+                     "first_launch_frac_fp16_peak": round(fl / t1 / 1e12 / PEAK_FP16_TFLOPS, 4)}
     return res
 
 
@@ -442,7 +539,8 @@ def config_encoder_attention(torch, stream, q8, reps=50):
 
 
 CONFIGS = {
-    "encoder_window": config_encoder_window, "batched_decode": config_batched_decode,
+    "encoder_window": config_encoder_window,
+    "encoder_window_engine": config_encoder_window_engine, "batched_decode": config_batched_decode,
     "decode_token": config_decode_token, "prefill": config_prefill,
     "long_audio": config_long_audio, "encoder_attention": config_encoder_attention,
 }
@@ -590,6 +688,8 @@ def main():
     if not args.no_configs:
         log("encoder window (32 layers x 4 GEMMs at M=1500)")
         cfg = {"encoder_window": config_encoder_window(torch, stream, q8)}
+        log("encoder window as the engine issues it (32 layers x 6 GEMMs at M=1500)")
+        cfg["encoder_window_engine"] = config_encoder_window_engine(torch, stream, q8)
         log("batched decode (M=8, 16)")
         cfg["batched_decode"] = config_batched_decode(torch, stream, q8)
         log("decoder token (M=1, GEMV family)")

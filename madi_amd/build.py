@@ -37,8 +37,23 @@ HIP_FLAGS = [
 ]
 
 
+ISSUE_SRC = os.path.join(CSRC, "issue.c")
+ISSUE_LIB = os.path.join(HERE, "libmadi_issue.so")
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+
+def build_issue(lib: str = LIB, out: str = ISSUE_LIB) -> str:
+    """The compiled issue loop (csrc/issue.c) that bench.py uses to replay a
+    call list from C, linked against the library it calls."""
+    tmp = out + ".tmp"
+    _run(["gcc", "-O2", "-std=c11", "-shared", "-fPIC", "-Wall", "-I", os.path.join(ROOT, "include"),
+          ISSUE_SRC, "-o", tmp, "-L", os.path.dirname(lib), "-l:" + os.path.basename(lib),
+          "-Wl,-rpath,$ORIGIN"])
+    os.replace(tmp, out)
+    return out
 
 
 def _run(cmd):
@@ -68,6 +83,8 @@ def build(verbose: bool = False, extra_flags=(), out: str = LIB, obj_dir: str = 
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs,
           "-L/opt/rocm/lib", "-lrocblas", "-Wl,-rpath,/opt/rocm/lib"])
     os.replace(tmp, out)
+    if out == LIB:
+        build_issue()
     return out
 
 

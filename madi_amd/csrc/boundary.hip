@@ -71,11 +71,19 @@ constexpr FnName kFunctions[] = {
     {"m4_flash_enc", kFnFlashEnc},       {"flash_attention_enc_f16", kFnFlashEnc},
 };
 
+// One recorded kDeq.  [lo, hi) is the byte range of wdq still owed the
+// dequantised weights: all of it when recorded; a later write by this library
+// that covers one end of the range (the encoder's next, smaller kDeq into the
+// same scratch, encoder.zig:262-265 after :297) moves that end instead of
+// writing the weights out first.  A record whose range is no longer all of
+// wdq serves no fused GEMM; it is only carried out (over its range) if
+// something observes that range.
 struct Deferred {
   uintptr_t wdq;        // F16 [K][N] destination, 2*n*k bytes
   const void *qs, *sc;  // panel-layout Q8 source
   uint32_t n, k;
-  bool pending;  // wdq not written yet
+  bool pending;   // the range not written yet
+  size_t lo, hi;  // byte range of wdq owed the weights
 };
 std::vector<Deferred> g_def;
 bool g_defer = true;
@@ -83,6 +91,10 @@ bool g_defer = true;
 bool overlaps(uintptr_t a, size_t an, uintptr_t b, size_t bn) { return a < b + bn && b < a + an; }
 
 size_t wdq_bytes(const Deferred &d) { return (size_t)d.n * d.k * 2; }
+bool whole(const Deferred &d) { return d.lo == 0 && d.hi == wdq_bytes(d); }
+bool range_overlaps(const Deferred &d, uintptr_t p, size_t bytes) {
+  return overlaps(d.wdq + d.lo, d.hi - d.lo, p, bytes);
+}
 
 bool source_overlaps(const Deferred &d, uintptr_t p, size_t bytes) {
   return overlaps(reinterpret_cast<uintptr_t>(d.qs), (size_t)d.n * d.k, p, bytes) ||
@@ -91,7 +103,10 @@ bool source_overlaps(const Deferred &d, uintptr_t p, size_t bytes) {
 
 int materialize(Deferred &d) {
   if (!d.pending) return MADI_OK;
-  if (int rc = dequant_launch(reinterpret_cast<void *>(d.wdq), d.qs, d.sc, d.n, d.k)) return rc;
+  // lo and hi are even (element boundaries) by construction
+  if (int rc = dequant_launch(reinterpret_cast<void *>(d.wdq), d.qs, d.sc, d.n, d.k, d.lo / 2,
+                              d.hi / 2))
+    return rc;
   d.pending = false;
   return MADI_OK;
 }
@@ -109,17 +124,36 @@ int deferred_before_write(const void *ptr, size_t bytes) {
   for (size_t i = 0; i < g_def.size();) {
     Deferred &d = g_def[i];
     const bool src = source_overlaps(d, p, bytes);
-    const bool dst = overlaps(d.wdq, wdq_bytes(d), p, bytes);
+    const bool dst = range_overlaps(d, p, bytes);
     if (!src && !dst) {
       ++i;
       continue;
     }
-    // The Q8 source is about to change, or part of wdq is about to be
-    // overwritten: wdq gets its dequantisation first (the write then lands on
-    // top of it).  A write that covers all of wdq makes the record moot.
-    const bool covers = p <= d.wdq && d.wdq + wdq_bytes(d) <= p + bytes;
-    if (src || !covers)
-      if (int rc = materialize(d)) return rc;
+    if (!src) {
+      // Part of the owed range is about to be overwritten.  A write over all
+      // of it makes the record moot; one over either end (at an element
+      // boundary) shortens the range; one inside it leaves two pieces, which
+      // are written out now (the write then lands on top).
+      const uintptr_t a = d.wdq + d.lo, b = d.wdq + d.hi;
+      const bool head = p <= a, tail = p + bytes >= b;
+      if (head && tail) {
+        retire(i);
+        continue;
+      }
+      if (head && (p + bytes - d.wdq) % 2 == 0) {
+        d.lo = p + bytes - d.wdq;
+        ++i;
+        continue;
+      }
+      if (tail && (p - d.wdq) % 2 == 0) {
+        d.hi = p - d.wdq;
+        ++i;
+        continue;
+      }
+    }
+    // The Q8 source is about to change, or the write splits the range:
+    // wdq gets its weights now.
+    if (int rc = materialize(d)) return rc;
     retire(i);
   }
   return MADI_OK;
@@ -131,7 +165,7 @@ int deferred_before_free(const void *ptr, size_t bytes) {
   int launched = 0;
   for (size_t i = 0; i < g_def.size();) {
     Deferred &d = g_def[i];
-    const bool dst = overlaps(d.wdq, wdq_bytes(d), p, bytes);
+    const bool dst = range_overlaps(d, p, bytes);
     const bool src = source_overlaps(d, p, bytes);
     if (!src && !dst) {
       ++i;
@@ -151,7 +185,7 @@ int deferred_before_read(const void *ptr, size_t bytes) {
   if (g_def.empty() || !ptr) return MADI_OK;
   const uintptr_t p = reinterpret_cast<uintptr_t>(ptr);
   for (Deferred &d : g_def)
-    if (d.pending && overlaps(d.wdq, wdq_bytes(d), p, bytes))
+    if (d.pending && range_overlaps(d, p, bytes))
       if (int rc = materialize(d)) return rc;
   return MADI_OK;
 }
@@ -159,7 +193,7 @@ int deferred_before_read(const void *ptr, size_t bytes) {
 bool deferred_lookup(const void *wdq, uint32_t n, uint32_t k, const void **qs, const void **sc) {
   const uintptr_t p = reinterpret_cast<uintptr_t>(wdq);
   for (const Deferred &d : g_def)
-    if (d.wdq == p && d.n == n && d.k == k) {
+    if (d.wdq == p && d.n == n && d.k == k && whole(d)) {
       *qs = d.qs;
       *sc = d.sc;
       return true;
@@ -172,7 +206,7 @@ int deferred_record(void *wdq, const void *qs, const void *sc, uint32_t n, uint3
   // overlaps) are retired first
   if (int rc = deferred_before_write(wdq, (size_t)n * k * 2)) return rc;
   if (!g_defer) return 0;
-  g_def.push_back({reinterpret_cast<uintptr_t>(wdq), qs, sc, n, k, true});
+  g_def.push_back({reinterpret_cast<uintptr_t>(wdq), qs, sc, n, k, true, 0, (size_t)n * k * 2});
   return 1;
 }
 
@@ -204,8 +238,11 @@ extern "C" int madi_q8_materialize(void *wdq) {
       if (int rc = materialize(d)) return rc;
     return MADI_OK;
   }
+  // every record naming wdq (a shortened one and the later kDeq that
+  // shortened it own disjoint ranges)
   for (Deferred &d : g_def)
-    if (d.wdq == reinterpret_cast<uintptr_t>(wdq)) return materialize(d);
+    if (d.wdq == reinterpret_cast<uintptr_t>(wdq))
+      if (int rc = materialize(d)) return rc;
   return MADI_OK;
 }
 

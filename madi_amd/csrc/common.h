@@ -59,7 +59,9 @@ int deferred_before_free(const void *ptr, size_t bytes);
 // Materialises every record and forgets them (madi_cleanup).
 int deferred_flush_all();
 // Launches the transposed dequantisation Q8 -> F16 [K][N] (layout.hip).
-int dequant_launch(void *wdq, const void *qs, const void *sc, uint32_t n, uint32_t k);
+// dequantise into wdq the elements with index in [lo, hi) (layout.hip)
+int dequant_launch(void *wdq, const void *qs, const void *sc, uint32_t n, uint32_t k, size_t lo,
+                   size_t hi);
 // Bytes from p to the end of the live madi_alloc allocation that contains p,
 // 0 if no such allocation contains it.
 size_t alloc_extent(const void *p);

@@ -14,7 +14,8 @@
 // 51866-row vocab matrix (1621 panels, seven per CU) is resident from the
 // start.
 //
-// The activation vector is loaded before the weights, staged once per
+// The activation vector is loaded next to the first weight window (before
+// it for the narrow matrices, after it for the vocab), staged once per
 // workgroup in LDS and read back as broadcast 128-bit LDS loads.  v_perm_b32
 // turns two stored bytes u = q + 128 into the fp16 pair 1024 + u and one
 // packed subtract of 1152 leaves the exact fp16 pair (q0, q1); fp16
@@ -46,6 +47,7 @@ constexpr uint32_t kWidePanels = 256;
 // slower (the waves then sit blocked on issue and compute in one late burst).
 constexpr int kWin = 2;
 constexpr uint32_t kMaxK = 12288;
+
 
 enum GemvMode { kPlain = 0, kBias = 1, kBiasGelu = 2, kBiasRes = 3, kQkv = 4 };
 
@@ -163,15 +165,24 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(7))) vo
   const uint32_t nck = cper + (split < crem ? 1 : 0);
   const uint32_t c0 = cs + (wave * nck) / KW, c1 = cs + ((wave + 1) * nck) / KW;
 
-  // ---- x: load first (16 bytes per thread and piece), then the weights.
-  // Lanes past a partial panel's last row read row R-1 (in bounds; their sums
-  // are never stored).
+  // ---- x (16 bytes per thread and piece) and the first weight window.
+  // Narrow matrices (sixteen waves, one or two chunks each) load x first: its
+  // staging barrier, not the weights, is then the longer wait.  The vocab
+  // matrix (four waves, five chunks each) issues its first weight window
+  // first, so the HBM requests leave before the L2-resident vector's
+  // (alternating runs in one process: 12.16 -> 11.92 us with f16 x, 12.66 ->
+  // 12.35 us with f32 x; the narrow ones measured slower that way, a decoder
+  // token 126 -> 134 us).  Lanes past a partial panel's last row read row R-1
+  // (in bounds; their sums are never stored).
+  constexpr bool kWeightsFirst = KW == kWaves;
   const uint32_t pieces = K * sizeof(XT) / 16;
   const rsrc_t xr = make_rsrc(a.x, K * sizeof(XT));
   u32x4 xv0 = {}, xv1 = {};
   const uint32_t i0 = threadIdx.x, i1 = threadIdx.x + KW * 64;
-  if (i0 < pieces) xv0 = __builtin_amdgcn_raw_buffer_load_b128(xr, i0 * 16, 0, 0);
-  if (i1 < pieces) xv1 = __builtin_amdgcn_raw_buffer_load_b128(xr, i1 * 16, 0, 0);
+  if constexpr (!kWeightsFirst) {
+    if (i0 < pieces) xv0 = __builtin_amdgcn_raw_buffer_load_b128(xr, i0 * 16, 0, 0);
+    if (i1 < pieces) xv1 = __builtin_amdgcn_raw_buffer_load_b128(xr, i1 * 16, 0, 0);
+  }
 
   const rsrc_t wq = make_rsrc(a.qs, a.n * K), ws = make_rsrc(a.sc, a.n * (K / 32) * 2);
   // chunks past the wave's range load through an empty resource: no memory
@@ -183,12 +194,16 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(7))) vo
   const rsrc_t wz = make_rsrc(a.qs, 0);
   const uint32_t rr = live ? r : R - 1;
   const uint32_t w_voff = (h * R + rr) * 16, s_voff = (h * R + rr) * 2;
-  // the first kWin chunks of this wave's range go in flight behind x
+  // the first kWin chunks of this wave's range
   ChunkW win[kWin];
 #pragma unroll
   for (int k = 0; k < kWin; ++k) {
     const bool in = c0 + k < c1;
     load_chunk(win[k], in ? wq : wz, in ? ws : wz, K, c0 + k, p, R, w_voff, s_voff);
+  }
+  if constexpr (kWeightsFirst) {
+    if (i0 < pieces) xv0 = __builtin_amdgcn_raw_buffer_load_b128(xr, i0 * 16, 0, 0);
+    if (i1 < pieces) xv1 = __builtin_amdgcn_raw_buffer_load_b128(xr, i1 * 16, 0, 0);
   }
 
   // The epilogue's operands (bias, residual, q/v bias, cache position) load

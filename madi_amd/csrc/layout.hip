@@ -224,11 +224,14 @@ extern "C" uint64_t madi_q8_fnv(uint64_t seed, const void *qs, size_t nq, const 
 // ------------------------------------------------------------------ dequant -> F16 [K][N]
 // grid (ceil(R*K/16 / 256), panels): one thread per panel-layout 16-byte unit.
 // Consecutive lanes hold consecutive rows r, so each of the 16 stores writes
-// 32 consecutive n of one output row k (coalesced 64-byte runs).
+// 32 consecutive n of one output row k (coalesced 64-byte runs).  Only the
+// elements with index in [lo, hi) are written (the whole matrix, [0, n*k),
+// for kDeq; a window when part of the destination has since been overwritten).
 __global__ __launch_bounds__(256) void q8_dequant_f16_kernel(f16 *__restrict__ out,
                                                              const uint8_t *__restrict__ qs,
                                                              const f16 *__restrict__ sc,
-                                                             uint32_t n, uint32_t k) {
+                                                             uint32_t n, uint32_t k, size_t lo,
+                                                             size_t hi) {
   const uint32_t p = blockIdx.y, R = panel_rows(n, p);
   const uint32_t u = blockIdx.x * 256 + threadIdx.x;
   if (u >= R * (k / 16)) return;
@@ -237,24 +240,27 @@ __global__ __launch_bounds__(256) void q8_dequant_f16_kernel(f16 *__restrict__ o
   const uint32_t jh = rem / R, r = rem % R, j = jh / 2, h = jh % 2;
   const u32x4 w = *reinterpret_cast<const u32x4 *>(qs + panel_chunk_qs(k, p, R, c) + rem * 16);
   const f16 s = sc[panel_chunk_sc(k, p, R, c) + h * R + r];
-  f16x8 lo, hi;
-  dequant16(w, s, lo, hi);
+  f16x8 lo8, hi8;
+  dequant16(w, s, lo8, hi8);
   const uint32_t col = p * kPanelRows + r;
   const uint32_t k0 = c * kChunkK + h * 32 + j * 16;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    out[(size_t)(k0 + i) * n + col] = lo[i];
-    out[(size_t)(k0 + 8 + i) * n + col] = hi[i];
+    const size_t e0 = (size_t)(k0 + i) * n + col, e1 = (size_t)(k0 + 8 + i) * n + col;
+    if (e0 >= lo && e0 < hi) out[e0] = lo8[i];
+    if (e1 >= lo && e1 < hi) out[e1] = hi8[i];
   }
 }
 
 namespace madi {
-int dequant_launch(void *wdq, const void *qs, const void *scales, uint32_t n, uint32_t k) {
+int dequant_launch(void *wdq, const void *qs, const void *scales, uint32_t n, uint32_t k,
+                   size_t lo, size_t hi) {
   const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
   const uint32_t units = kPanelRows * (k / 16);
+  if (hi > (size_t)n * k) hi = (size_t)n * k;
   hipLaunchKernelGGL(q8_dequant_f16_kernel, dim3((units + 255) / 256, np), dim3(256), 0,
                      stream(), static_cast<f16 *>(wdq), static_cast<const uint8_t *>(qs),
-                     static_cast<const f16 *>(scales), n, k);
+                     static_cast<const f16 *>(scales), n, k, lo, hi);
   return check_launch("madi_q8_dequant_f16");
 }
 }  // namespace madi
@@ -271,7 +277,7 @@ extern "C" int madi_q8_dequant_f16(void *wdq, const void *qs, const void *scales
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_dequant_f16: madi_init has not succeeded");
   const int rec = deferred_record(wdq, qs, scales, n, k);
   if (rec != 0) return rec < 0 ? rec : MADI_OK;
-  return dequant_launch(wdq, qs, scales, n, k);
+  return dequant_launch(wdq, qs, scales, n, k, 0, (size_t)n * k);
 }
 
 // ------------------------------------------------------------------ embedding rows

@@ -428,12 +428,15 @@ def test_outside_writes_announced_with_forget(q):
     q.sync()
     ref = a.astype(np.float64) @ w16.astype(np.float64)
     assert normwise(host_f16(c), ref) <= TOL
-    # 2. partial overwrite: the untouched part holds the dequantised weights
+    # 2. partial overwrite of the head: the record shrinks to the rest, which
+    # a reader outside the library gets with madi_q8_materialize (the head
+    # written from torch is left alone)
     wdq = sentinel(k * n)
     q.kDeq(wdq, w, n, k)
     head = wdq[:64]
     q.forget(head)
     head.copy_(torch.arange(64, dtype=torch.int16, device="cuda"))
+    q.materialize(wdq)
     q.sync()
     got = wdq.cpu().numpy().view(np.uint16)
     assert np.array_equal(got[:64], np.arange(64, dtype=np.uint16))
@@ -447,3 +450,83 @@ def test_outside_writes_announced_with_forget(q):
     qt.zero_()
     q.sync()
     assert np.array_equal(wdq.cpu().numpy().view(np.uint16), want)
+
+
+def test_issue_list_replays_the_engine_layer(q):
+    """The encoder layer of test_encoder_layer_unchanged_sequence recorded in
+    an IssueList and replayed from C (the bench's issue path) gives the same
+    bits as the calls made one by one from Python."""
+    say("issue list replay of one encoder layer")
+    from madi_amd.issue import IssueList
+    rng = np.random.default_rng(2626)
+    m = 700
+    qkv_w = q.upload_q8(*synth.q8_weight(rng, 3 * D, D))
+    m0_w = q.upload_q8(*synth.q8_weight(rng, MLP, D))
+    m2_w = q.upload_q8(*synth.q8_weight(rng, D, MLP))
+    qb, m0b = dev(rng.standard_normal(D).astype(np.float32)), dev(rng.standard_normal(MLP).astype(np.float32))
+    x = dev_f16(synth.activations(rng, m, D))
+    wdq, wdq2 = sentinel(D * MLP), sentinel(D * MLP)
+    outs = []
+    for how in ("python", "c"):
+        qo = torch.empty((m, D), dtype=torch.int16, device="cuda")
+        ko = torch.empty((m, D), dtype=torch.int16, device="cuda")
+        mh = torch.empty((m, MLP), dtype=torch.int16, device="cuda")
+        mo = torch.empty((m, D), dtype=torch.int16, device="cuda")
+        lst = IssueList() if how == "c" else q
+        lst.kDeq(wdq, qkv_w, D, D)
+        lst.kM4Bias(q.getFunction("m4_gemm_bias"), x, wdq, qo, qb, m, D, D)
+        lst.kDeq(wdq2, qkv_w.rows(D, D), D, D)
+        lst.kM4Bias(q.getFunction("m4_gemm_bias"), x, wdq2, ko, qb, m, D, D)
+        lst.kDeq(wdq, m0_w, MLP, D)
+        lst.kM4Bias(q.getFunction("m4_gemm_bias_gelu"), x, wdq, mh, m0b, m, MLP, D)
+        lst.kDeq(wdq2, m2_w, D, MLP)
+        lst.kM4(q.getFunction("m4_gemm_nn"), mh, wdq2, mo, m, D, MLP)
+        if how == "c":
+            lst.run(2)
+        q.sync()
+        outs.append([t.cpu().numpy() for t in (qo, ko, mh, mo)])
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)
+    assert np.all(wdq.cpu().numpy().view(np.uint16) == NAN16)
+
+
+def test_smaller_kdeq_shortens_the_earlier_record(q):
+    """The encoder's scratch pattern: kDeq of fc1 (5120 x 1280) into wdq, then
+    the next layer's kDeq of q (1280 x 1280) into the start of the same
+    buffer.  The second record takes the head; the first keeps the rest
+    without writing it (the fused GEMM on the second still runs and wdq stays
+    a sentinel), and whatever reads wdq later sees exactly what the two kDeq
+    calls would have left there: q's weights, then the tail of fc1's."""
+    say("smaller kDeq over an earlier record")
+    rng = np.random.default_rng(297)
+    big_q, big_s = synth.q8_weight(rng, MLP, D)
+    sm_q, sm_s = synth.q8_weight(rng, D, D)
+    big, sm = q.upload_q8(big_q, big_s), q.upload_q8(sm_q, sm_s)
+    wdq = sentinel(D * MLP)
+    m = 64
+    a = synth.activations(rng, m, D)
+    c = torch.empty((m, D), dtype=torch.int16, device="cuda")
+    q.kDeq(wdq, big, MLP, D)
+    q.kDeq(wdq, sm, D, D)
+    q.kM4("m4_gemm_nn", dev_f16(a), wdq, c, m, D, D)
+    q.sync()
+    assert np.all(wdq.cpu().numpy().view(np.uint16) == NAN16)
+    assert normwise(host_f16(c).astype(np.float64), O.q8_gemm_rows(a, sm_q, sm_s)) <= TOL
+    q.materialize(wdq)
+    q.sync()
+    got = wdq.cpu().numpy().view(np.uint16)
+    head = O.dequant_q8_f16(sm_q, sm_s).view(np.uint16).reshape(-1)
+    tail = O.dequant_q8_f16(big_q, big_s).view(np.uint16).reshape(-1)
+    assert np.array_equal(got[:D * D], head)
+    assert np.array_equal(got[D * D:], tail[D * D:])
+    # a write strictly inside an owed range splits it: the weights are written
+    # out at once and the write lands on top
+    wdq2 = DevBuf(D * D * 2)
+    _lib.call("madi_q8_dequant_f16", wdq2.p, sm.qs, sm.scales, D, D)
+    mid = np.full(16, 7, np.uint16)
+    _lib.call("madi_upload", wdq2.p + 4096, mid.ctypes.data, mid.nbytes)
+    got2 = wdq2.down(np.uint16, D * D)
+    want2 = head.copy()
+    want2[2048:2064] = 7
+    assert np.array_equal(got2, want2)
+    wdq2.free()
