@@ -228,8 +228,11 @@ def config_encoder_window_engine(torch, stream, q8, reps=3):
     1280->1280 GEMMs + bias from row slices of the stacked q|k|v weight into
     the three blocks of s.qkv, out-proj 1280->1280 without bias, fc1
     1280->5120 + bias + GELU, fc2 5120->1280 without bias (its bias goes into
-    the next layer norm).  32 layers, independent weights, M = 1500, issued
-    from C through the boundary (madi_m4_gemm on the recorded scratch)."""
+    the next layer norm).  32 layers, independent weights (each in its own
+    madi_alloc allocation, as the engine's loader makes them), M = 1500,
+    issued from C through the boundary (madi_m4_gemm on the recorded
+    scratch; the q, k, v calls run as one grouped launch).  Also timed with
+    the grouping off (three launches)."""
     from madi_amd import synth
     from madi_amd.issue import IssueList
     m, d, mlp = 1500, DIM, 5120
@@ -243,11 +246,15 @@ def config_encoder_window_engine(torch, stream, q8, reps=3):
     wdq = torch.empty(d * mlp, dtype=torch.int16, device="cuda")     # Scratch.wdq
     wdq2 = torch.empty(d * mlp, dtype=torch.int16, device="cuda")    # Scratch.wdq2
     m4, m4b, m4bg = (q8.getFunction(nm) for nm in ("m4_gemm_nn", "m4_gemm_bias", "m4_gemm_bias_gelu"))
+    from madi_amd import synth as _s
+
+    def alloc_layer(seed, n, k):  # each weight in its own madi_alloc allocation, as the loader
+        return q8.upload_q8_alloc(*_s.q8_weight(np.random.default_rng(seed), n, k))
     layers = []
     for l in range(ENC_LAYERS):
         layers.append(dict(
-            qkv=_upload_layer(q8, 6000 + 8 * l, 3 * d, d), o=_upload_layer(q8, 6001 + 8 * l, d, d),
-            m0=_upload_layer(q8, 6002 + 8 * l, mlp, d), m2=_upload_layer(q8, 6003 + 8 * l, d, mlp),
+            qkv=alloc_layer(6000 + 8 * l, 3 * d, d), o=alloc_layer(6001 + 8 * l, d, d),
+            m0=alloc_layer(6002 + 8 * l, mlp, d), m2=alloc_layer(6003 + 8 * l, d, mlp),
             qb=f32(d), kb=f32(d), vb=f32(d), m0b=f32(mlp)))
     torch.cuda.synchronize()
     q_, k_, v_ = (qkv[i] for i in range(3))
@@ -266,13 +273,19 @@ def config_encoder_window_engine(torch, stream, q8, reps=3):
         window.kDeq(wdq2, L["m2"], d, mlp)
         window.kM4(m4, mh, wdq2, mo, m, d, mlp)
     t = _timed_list(torch, stream, window, reps)
+    q8.set_gemm_grouping(False)   # q, k, v as three launches, for comparison
+    t3 = _timed_list(torch, stream, window, reps)
+    q8.set_gemm_grouping(True)
     flops = ENC_LAYERS * 2.0 * m * (4 * d * d + 2 * d * mlp)
     del layers
     return {
+        "ungrouped_ms_per_window": round(t3 * 1e3, 4),
+        "ungrouped_frac_fp16_peak": round(flops / t3 / 1e12 / PEAK_FP16_TFLOPS, 4),
         "workload": "32 layers x (q, k, v 1280->1280 +bias from slices of the stacked weight, "
                     "out 1280->1280, fc1 1280->5120 +bias+GELU, fc2 5120->1280) at M=1500 as "
                     "encoder.zig:256-303 issues them (kDeq + kM4/kM4Bias handles through the "
-                    "deferred dequantisation), independent weights per layer, issued from C",
+                    "deferred dequantisation, q|k|v grouped into one launch), independent "
+                    "weights per layer, issued from C",
         "ms_per_window": round(t * 1e3, 4), "tflop_per_window": round(flops / 1e12, 4),
         "tflops": round(flops / t / 1e12, 1),
         "frac_fp16_peak": round(flops / t / 1e12 / PEAK_FP16_TFLOPS, 4),

@@ -255,6 +255,22 @@ int madi_q8_materialize(void *wdq);
 int madi_q8_forget(void *ptr, size_t bytes);
 int madi_set_deferred_dequant(int on);
 
+/* q|k|v grouping.  The encoder computes q, k and v as three F16 GEMMs on the
+ * same activations, each on a kDeq of the next 1280-row slice of the stacked
+ * q|k|v weight (encoder.zig:262-267).  With grouping on (the default), an
+ * F16 GEMM that runs the fused Q8 kernel on the FIRST slice of a stacked
+ * weight (its Q8 source at the start of a madi_alloc allocation holding at
+ * least three such slices) is held; the GEMMs on the following slices with
+ * the same activations, shape and epilogue join it, and the three run as one
+ * launch of the stacked GEMM writing the three outputs once the last slice
+ * arrives (the allocation's end or the third).  Any library call that reads
+ * a held output or writes a held operand, madi_sync, madi_commit_command_buffer,
+ * madi_set_stream and madi_q8_materialize launch a held group first.  Code
+ * outside this library that reads q or k before the v GEMM has been issued
+ * calls madi_sync first, or turns grouping off with madi_set_gemm_grouping(0)
+ * (which launches a held group).  No counterpart in the reference. */
+int madi_set_gemm_grouping(int on);
+
 /* ---- plain fp16 GEMMs (pre-dequantised F16 weights) ------------------------ */
 /* C[M][N] (f16) = epi(A[M][K] (f16) . B[K][N] (f16)), all row-major, fp32
  * accumulation.  Replaces kM4 / kM4Bias (engine/metal/encoder.zig:125-136) ->

@@ -62,6 +62,7 @@ SIGNATURES = {
     "madi_q8_materialize": (_I, [_P]),
     "madi_q8_forget": (_I, [_P, _SZ]),
     "madi_set_deferred_dequant": (_I, [_I]),
+    "madi_set_gemm_grouping": (_I, [_I]),
     "madi_f16_gemm": (_I, [_P, _P, _P, _P, _U32, _U32, _U32, _I]),
     "madi_matmul_f16": (_I, [_P, _P, _P, _I, _I, _I, ctypes.c_float, ctypes.c_float]),
     "madi_q8_emb_lookup": (_I, [_P, _P, _P, _P, _U32, _U32]),

@@ -111,7 +111,109 @@ int materialize(Deferred &d) {
   return MADI_OK;
 }
 
+// ---- q|k|v as one launch.  The encoder computes q, k and v as three GEMMs
+// on the same activations (encoder.zig:262-267): kDeq of a 1280-row slice of
+// the stacked q|k|v weight, then kM4Bias into its own output, three times.
+// A fused GEMM whose weight is the first slice of a stacked weight (a
+// madi_alloc allocation holding at least three such slices) is held back;
+// the next fused GEMMs with the same activations, shape and epilogue on the
+// following slices join it, and the group runs as one launch of the stacked
+// GEMM with three outputs once its last slice (the allocation's end, or the
+// third) arrives.  Anything else that touches the group's memory -- a read
+// of an output, a write of any operand -- or a sync, commit or stream change
+// launches the group first.  Code outside this library that reads q or k
+// before the v GEMM has been issued must call madi_sync (or
+// madi_set_gemm_grouping(0)); the engine reads them only in kFlash, after v.
+struct PendingGemm {
+  const void *a, *qs, *sc;
+  void *c;
+  const float *bias;
+  uint32_t m, n, k;
+  int epi;
+};
+PendingGemm g_grp[kMaxSegs];
+int g_ngrp = 0;
+bool g_grouping = true;
+
+bool group_touches(uintptr_t p, size_t bytes, bool write) {
+  for (int i = 0; i < g_ngrp; ++i) {
+    const PendingGemm &g = g_grp[i];
+    if (overlaps(reinterpret_cast<uintptr_t>(g.c), (size_t)g.m * g.n * 2, p, bytes)) return true;
+    if (!write) continue;
+    if (overlaps(reinterpret_cast<uintptr_t>(g.a), (size_t)g.m * g.k * 2, p, bytes) ||
+        overlaps(reinterpret_cast<uintptr_t>(g.qs), (size_t)g.n * g.k, p, bytes) ||
+        overlaps(reinterpret_cast<uintptr_t>(g.sc), (size_t)g.n * (g.k / 32) * 2, p, bytes) ||
+        (g.bias && overlaps(reinterpret_cast<uintptr_t>(g.bias), (size_t)g.n * 4, p, bytes)))
+      return true;
+  }
+  return false;
+}
+
 }  // namespace
+
+// Launches the held q|k|v group (as one GEMM with an output per slice where
+// the shape's kernel allows it, else one GEMM per slice).
+int group_flush() {
+  if (g_ngrp == 0) return MADI_OK;
+  PendingGemm g[kMaxSegs];
+  const int cnt = g_ngrp;
+  for (int i = 0; i < cnt; ++i) g[i] = g_grp[i];
+  g_ngrp = 0;  // the launches below check their operands against no group
+  if (cnt > 1) {
+    OutSeg seg{};
+    seg.n = g[0].n;
+    for (int i = 0; i < cnt; ++i) {
+      seg.c[i] = g[i].c;
+      seg.b[i] = g[i].bias;
+    }
+    const int rc = q8_gemm_seg(g[0].a, g[0].qs, g[0].sc, seg, g[0].m, g[0].n * cnt, g[0].k, g[0].epi);
+    if (rc != kSegUnsupported) return rc;
+  }
+  for (int i = 0; i < cnt; ++i)
+    if (int rc = madi_q8_gemm(g[i].a, g[i].qs, g[i].sc, g[i].c, g[i].bias, g[i].m, g[i].n, g[i].k,
+                              g[i].epi))
+      return rc;
+  return MADI_OK;
+}
+
+// The fused route of the F16 GEMM entry points (a recorded wdq as the weight):
+// joins, holds or launches, as described above.
+int fused_gemm(const void *a, const void *qs, const void *sc, void *c, const float *bias, uint32_t m,
+               uint32_t n, uint32_t k, int epi) {
+  const uintptr_t ua = reinterpret_cast<uintptr_t>(a), uc = reinterpret_cast<uintptr_t>(c);
+  const size_t abytes = (size_t)m * k * 2, cbytes = (size_t)m * n * 2;
+  const size_t qbytes = (size_t)n * k, sbytes = (size_t)n * (k / 32) * 2;
+  if (g_ngrp > 0) {
+    const PendingGemm &f = g_grp[0], &l = g_grp[g_ngrp - 1];
+    bool join = g_grouping && g_ngrp < kMaxSegs && a == f.a && m == f.m && n == f.n && k == f.k &&
+                epi == f.epi &&
+                qs == static_cast<const uint8_t *>(l.qs) + qbytes &&
+                sc == static_cast<const uint8_t *>(l.sc) + sbytes && !overlaps(uc, cbytes, ua, abytes);
+    for (int i = 0; join && i < g_ngrp; ++i)
+      join = !overlaps(uc, cbytes, reinterpret_cast<uintptr_t>(g_grp[i].c), cbytes);
+    if (join) {
+      if (int rc = deferred_before_write(c, cbytes)) return rc;
+      // (that write could touch the group's weights or bias and launch it;
+      // then this GEMM is no longer part of a group)
+      if (g_ngrp > 0) {
+        g_grp[g_ngrp++] = {a, qs, sc, c, bias, m, n, k, epi};
+        if (g_ngrp == kMaxSegs || alloc_extent(qs) < 2 * qbytes) return group_flush();
+        return MADI_OK;
+      }
+    } else if (int rc = group_flush()) {
+      return rc;
+    }
+  }
+  if (g_grouping && alloc_extent(qs) >= 3 * qbytes && alloc_extent(sc) >= 3 * sbytes &&
+      !overlaps(uc, cbytes, ua, abytes)) {
+    if (int rc = deferred_before_read(a, abytes)) return rc;
+    if (int rc = deferred_before_write(c, cbytes)) return rc;
+    g_grp[0] = {a, qs, sc, c, bias, m, n, k, epi};
+    g_ngrp = 1;
+    return MADI_OK;
+  }
+  return madi_q8_gemm(a, qs, sc, c, bias, m, n, k, epi);
+}
 
 static void retire(size_t i) {
   g_def[i] = g_def.back();
@@ -119,6 +221,8 @@ static void retire(size_t i) {
 }
 
 int deferred_before_write(const void *ptr, size_t bytes) {
+  if (g_ngrp && ptr && group_touches(reinterpret_cast<uintptr_t>(ptr), bytes, true))
+    if (int rc = group_flush()) return rc;
   if (g_def.empty() || !ptr) return MADI_OK;
   const uintptr_t p = reinterpret_cast<uintptr_t>(ptr);
   for (size_t i = 0; i < g_def.size();) {
@@ -160,9 +264,13 @@ int deferred_before_write(const void *ptr, size_t bytes) {
 }
 
 int deferred_before_free(const void *ptr, size_t bytes) {
-  if (g_def.empty() || !ptr) return MADI_OK;
-  const uintptr_t p = reinterpret_cast<uintptr_t>(ptr);
   int launched = 0;
+  if (g_ngrp && ptr && group_touches(reinterpret_cast<uintptr_t>(ptr), bytes, true)) {
+    if (int rc = group_flush()) return rc;
+    launched = 1;
+  }
+  if (g_def.empty() || !ptr) return launched;
+  const uintptr_t p = reinterpret_cast<uintptr_t>(ptr);
   for (size_t i = 0; i < g_def.size();) {
     Deferred &d = g_def[i];
     const bool dst = range_overlaps(d, p, bytes);
@@ -182,6 +290,8 @@ int deferred_before_free(const void *ptr, size_t bytes) {
 }
 
 int deferred_before_read(const void *ptr, size_t bytes) {
+  if (g_ngrp && ptr && group_touches(reinterpret_cast<uintptr_t>(ptr), bytes, false))
+    if (int rc = group_flush()) return rc;
   if (g_def.empty() || !ptr) return MADI_OK;
   const uintptr_t p = reinterpret_cast<uintptr_t>(ptr);
   for (Deferred &d : g_def)
@@ -211,6 +321,7 @@ int deferred_record(void *wdq, const void *qs, const void *sc, uint32_t n, uint3
 }
 
 int deferred_flush_all() {
+  if (int rc = group_flush()) return rc;
   for (Deferred &d : g_def)
     if (int rc = materialize(d)) return rc;
   g_def.clear();
@@ -233,6 +344,7 @@ extern "C" int madi_get_function(const char *name, int *out_id) {
 
 extern "C" int madi_q8_materialize(void *wdq) {
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_materialize: madi_init has not succeeded");
+  if (int rc = group_flush()) return rc;
   if (!wdq) {
     for (Deferred &d : g_def)
       if (int rc = materialize(d)) return rc;
@@ -255,7 +367,16 @@ extern "C" int madi_q8_forget(void *ptr, size_t bytes) {
   return deferred_before_write(ptr, bytes);
 }
 
+extern "C" int madi_set_gemm_grouping(int on) {
+  if (!on && initialized())
+    if (int rc = group_flush()) return rc;
+  g_grouping = on != 0;
+  return MADI_OK;
+}
+
 extern "C" int madi_set_deferred_dequant(int on) {
+  if (initialized())
+    if (int rc = group_flush()) return rc;
   if (!on && initialized())
     for (Deferred &d : g_def)
       if (int rc = materialize(d)) return rc;

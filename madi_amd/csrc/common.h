@@ -35,6 +35,23 @@ int q8_skinny_f16io(const void *in, const void *qs, const void *scales, void *ou
 bool skinny_f16_ok(const void *in, const void *qs, const void *out, uint32_t m, uint32_t n,
                    uint32_t k);
 bool skinny_f16_prefers_gemm(uint32_t m, uint32_t n, uint32_t k);
+// Several outputs of one Q8 GEMM: columns [s*n, (s+1)*n) of the product go to
+// c[s] (row pitch n, f16) with bias b[s] -- the encoder's q, k and v
+// projections from one stacked weight, launched once into their three
+// buffers.  n == 0: a single output.
+constexpr int kMaxSegs = 3;
+struct OutSeg {
+  void *c[kMaxSegs];
+  const float *b[kMaxSegs];
+  uint32_t n;
+};
+// madi_q8_gemm into segments (gemm.hip).  Returns kSegUnsupported, having
+// launched nothing, where the shape's kernel writes one output only (K split
+// across workgroups, the in-workgroup K split, the persistent tile loop) or
+// the segment width is not a whole number of the launch's tiles.
+constexpr int kSegUnsupported = 1;
+int q8_gemm_seg(const void *a, const void *qs, const void *scales, const OutSeg &seg, uint32_t m,
+                uint32_t n, uint32_t k, int epilogue);
 // Resolves the current device's address of the allocation-free GEMM's fixed
 // scratch array and clears its counters (madi_init).
 int gemm_scratch_init();
@@ -58,6 +75,12 @@ int deferred_before_read(const void *ptr, size_t bytes);
 int deferred_before_free(const void *ptr, size_t bytes);
 // Materialises every record and forgets them (madi_cleanup).
 int deferred_flush_all();
+// The held q|k|v group (boundary.hip): launched now, if any.
+int group_flush();
+// The fused route of the F16 GEMM entry points on a recorded wdq: may hold
+// the GEMM to launch it together with the next q|k|v slices (boundary.hip).
+int fused_gemm(const void *a, const void *qs, const void *sc, void *c, const float *bias, uint32_t m,
+               uint32_t n, uint32_t k, int epi);
 // Launches the transposed dequantisation Q8 -> F16 [K][N] (layout.hip).
 // dequantise into wdq the elements with index in [lo, hi) (layout.hip)
 int dequant_launch(void *wdq, const void *qs, const void *sc, uint32_t n, uint32_t k, size_t lo,

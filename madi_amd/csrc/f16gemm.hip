@@ -118,7 +118,7 @@ extern "C" int madi_f16_gemm(const void *a, const void *b, void *c, const float 
   // kernel's epilogue, m4_gemm.metal:180-186) and b is never written
   const void *qs, *sc;
   if (fusable(a, c, bias, m, n, k) && deferred_lookup(b, n, k, &qs, &sc))
-    return madi_q8_gemm(a, qs, sc, c, bias, m, n, k, epilogue);
+    return fused_gemm(a, qs, sc, c, bias, m, n, k, epilogue);
   if (int rc = deferred_before_read(a, (size_t)m * k * 2)) return rc;
   if (int rc = deferred_before_read(b, (size_t)k * n * 2)) return rc;
   if (int rc = deferred_before_write(c, (size_t)m * n * 2)) return rc;

@@ -698,12 +698,31 @@ __device__ inline void tail(uint8_t *smem, uint32_t c, uint32_t h, uint32_t r, u
 }
 
 
+// Where a tile's outputs go: the launch's C and bias, or, when the launch
+// writes several outputs (OutSeg: the encoder's q, k and v from one stacked
+// weight), the segment holding the tile's columns (segments are whole tiles
+// wide: the host checks), with its own pointers, row pitch and panel origin.
+struct OutTile {
+  void *c;
+  const float *b;
+  uint32_t n, p0, np;
+};
+__device__ inline OutTile out_tile(const OutSeg &seg, void *C, const float *bias, uint32_t N,
+                                   uint32_t p0) {
+  if (seg.n == 0) return {C, bias, N, p0, N / kPanelRows};
+  const uint32_t n0 = p0 * kPanelRows;
+  uint32_t s = 0;
+#pragma unroll
+  for (int i = 1; i < kMaxSegs; ++i) s += n0 >= i * seg.n ? 1u : 0u;
+  return {seg.c[s], seg.b[s], seg.n, p0 - s * (seg.n / kPanelRows), seg.n / kPanelRows};
+}
+
 template <int MT, int EPI, bool PADDED, bool F32 = false, bool TAIL = false, int PW = 2>
 __global__ __launch_bounds__(256) void q8_gemm_kernel(
     const void *__restrict__ A, const uint8_t *__restrict__ qs, const f16 *__restrict__ sc,
     uint32_t M, uint32_t N, uint32_t K, uint32_t tiles_m, uint32_t tiles_n, uint32_t splits,
     uint32_t cper, uint32_t crem, void *__restrict__ Cout, const float *__restrict__ bias,
-    float *__restrict__ ws, uint32_t *__restrict__ cnt) {
+    float *__restrict__ ws, uint32_t *__restrict__ cnt, const OutSeg seg) {
   using G = Geometry<MT, F32, PW>;
   static_assert(!F32 || EPI == MADI_EPI_NONE, "f32 output has no bias epilogue");
   static_assert(!TAIL || (!PADDED && !F32 && MT >= 2 && PW == 2), "the m-tile-major tail's shapes");
@@ -839,8 +858,9 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     } while (c + 2 * WD <= nchunks);
     if constexpr (TAIL) {
       // one K split (the host checks): the tile's epilogue is the tail's
-      tail<MT, EPI>(smem, c, h, r, wave, acc, w, af, r0, r1, r2, r3, static_cast<f16 *>(Cout),
-                    bias, M, N, m0, p0, np);
+      const OutTile ot = out_tile(seg, Cout, bias, N, p0);
+      tail<MT, EPI>(smem, c, h, r, wave, acc, w, af, r0, r1, r2, r3, static_cast<f16 *>(ot.c),
+                    ot.b, M, ot.n, m0, ot.p0, ot.np);
       return;
     } else {
       chunk<MT, F32, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
@@ -963,6 +983,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
       __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
   }
+  const OutTile ot = out_tile(seg, Cout, bias, N, p0);
   // The tile leaves through LDS one m-tile (32 rows) at a time: all waves
   // write their columns of m-tile i, meet, and each stores 8 of its rows
   // while the next m-tile is converted, so the stores (the HBM write rate
@@ -980,9 +1001,9 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     // each), a store instruction 2 / PW rows
     constexpr uint32_t kLanesPerRow = 32 * PW, kRowsPerStore = 2 / PW;
     const uint32_t col = lane % kLanesPerRow;
-    const uint32_t n = p0 * kPanelRows + col * 4;
+    const uint32_t n = ot.p0 * kPanelRows + col * 4;
     const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
-        static_cast<float *>(Cout) + (size_t)m0 * N, 0, (int)(rows * N * 4), 0x00020000);
+        static_cast<float *>(ot.c) + (size_t)m0 * ot.n, 0, (int)(rows * ot.n * 4), 0x00020000);
 #pragma unroll
     for (int i = 0; i < MT; ++i) {
 #pragma unroll
@@ -1000,25 +1021,25 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
       for (uint32_t j = 0; j < 8 / kRowsPerStore; ++j) {
         const uint32_t row = i * 32 + wave * 8 + j * kRowsPerStore + lane / kLanesPerRow;
         const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * G::kCPitch + col * 16);
-        if (n < N) __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * N + n) * 4, 0, kSc1);
+        if (n < ot.n) __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * ot.n + n) * 4, 0, kSc1);
       }
     }
     return;
   }
   // a row of the tile is 16 PW lanes' 16 bytes, a store instruction 4 / PW rows
   constexpr uint32_t kLanesPerRow = 16 * PW, kRowsPerStore = 4 / PW;
-  const uint32_t n = p0 * kPanelRows + (lane % kLanesPerRow) * 8;
+  const uint32_t n = ot.p0 * kPanelRows + (lane % kLanesPerRow) * 8;
   const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
-      static_cast<f16 *>(Cout) + (size_t)m0 * N, 0, (int)(rows * N * 2), 0x00020000);
+      static_cast<f16 *>(ot.c) + (size_t)m0 * ot.n, 0, (int)(rows * ot.n * 2), 0x00020000);
   f32x4 b4[PW][4];
   if constexpr (EPI != MADI_EPI_NONE) {
 #pragma unroll
     for (int t = 0; t < PW; ++t) {
-      uint32_t pb = p0 + PW * wave + t;
-      pb = pb < np ? pb : np - 1;  // clamped panels: bias read in bounds, result never stored
+      uint32_t pb = ot.p0 + PW * wave + t;
+      pb = pb < ot.np ? pb : ot.np - 1;  // clamped panels: bias read in bounds, result never stored
 #pragma unroll
       for (int g = 0; g < 4; ++g)
-        b4[t][g] = *reinterpret_cast<const f32x4 *>(bias + pb * kPanelRows + g * 8 + h * 4);
+        b4[t][g] = *reinterpret_cast<const f32x4 *>(ot.b + pb * kPanelRows + g * 8 + h * 4);
     }
   }
 #pragma unroll
@@ -1050,7 +1071,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
       const uint32_t row = i * 32 + wave * 8 + kRowsPerStore * j + lane / kLanesPerRow;
       const u32x4 v = *reinterpret_cast<const u32x4 *>(Ct + row * G::kCPitch +
                                                        (lane % kLanesPerRow) * 16);
-      if (n < N) __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * N + n) * 2, 0, kSc1);
+      if (n < ot.n) __builtin_amdgcn_raw_buffer_store_b128(v, cr, (row * ot.n + n) * 2, 0, kSc1);
     }
   }
 }
@@ -1720,11 +1741,13 @@ enum Scratch { kWorkspace = 0, kStatic = 1 };
 
 template <int MT, int EPI, bool F32 = false, int PW = 2>
 int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const float *bias,
-                uint32_t M, uint32_t N, uint32_t K, Scratch where) {
+                uint32_t M, uint32_t N, uint32_t K, Scratch where, const OutSeg &seg = OutSeg{}) {
   const uint32_t tiles_m = (M + 32 * MT - 1) / (32 * MT);
   const uint32_t tiles_n = (N + 128 * PW - 1) / (128 * PW);
   const uint32_t T = tiles_m * tiles_n, chunks = K / kChunkK;
   const uint32_t splits = split_count(T, chunks);
+  // segments: unsplit launches whose tiles do not straddle a segment boundary
+  if (seg.n && (splits != 1 || seg.n % (128 * PW) != 0)) return kSegUnsupported;
   float *ws = nullptr;
   uint32_t *cnt = nullptr;
   if (splits > 1) {
@@ -1751,7 +1774,7 @@ int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const 
   // (the kernel's XCD mapping)
   const auto go = [&](auto kernel) {
     hipLaunchKernelGGL(kernel, dim3((T * splits + 7) & ~7u), dim3(kWaves * 64), 0, stream(), A, qs,
-                       sc, M, N, K, tiles_m, tiles_n, splits, cper, crem, C, bias, ws, cnt);
+                       sc, M, N, K, tiles_m, tiles_n, splits, cper, crem, C, bias, ws, cnt, seg);
   };
   if constexpr (PW == 1) {
     // 128-column tiles: the host chooses them only for unpadded K loops, and
@@ -1774,20 +1797,22 @@ int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const 
 
 template <int MT, int PW = 2>
 int dispatch_epi(int epi, const f16 *A, const uint8_t *qs, const f16 *sc, f16 *C,
-                 const float *bias, uint32_t M, uint32_t N, uint32_t K, Scratch where) {
+                 const float *bias, uint32_t M, uint32_t N, uint32_t K, Scratch where,
+                 const OutSeg &seg) {
   switch (epi) {
   case MADI_EPI_NONE:
-    return launch_gemm<MT, MADI_EPI_NONE, false, PW>(A, qs, sc, C, bias, M, N, K, where);
+    return launch_gemm<MT, MADI_EPI_NONE, false, PW>(A, qs, sc, C, bias, M, N, K, where, seg);
   case MADI_EPI_BIAS:
-    return launch_gemm<MT, MADI_EPI_BIAS, false, PW>(A, qs, sc, C, bias, M, N, K, where);
+    return launch_gemm<MT, MADI_EPI_BIAS, false, PW>(A, qs, sc, C, bias, M, N, K, where, seg);
   case MADI_EPI_BIAS_GELU:
-    return launch_gemm<MT, MADI_EPI_BIAS_GELU, false, PW>(A, qs, sc, C, bias, M, N, K, where);
+    return launch_gemm<MT, MADI_EPI_BIAS_GELU, false, PW>(A, qs, sc, C, bias, M, N, K, where, seg);
   default: return fail(MADI_ERR_ARG, "madi_q8_gemm: unknown epilogue %d", epi);
   }
 }
 
 int q8_gemm(const char *what, const void *a, const void *qs, const void *scales, void *c,
-            const float *bias, uint32_t m, uint32_t n, uint32_t k, int epilogue, Scratch where) {
+            const float *bias, uint32_t m, uint32_t n, uint32_t k, int epilogue, Scratch where,
+            const OutSeg &seg = OutSeg{}) {
   if (!a || !qs || !scales || !c) return fail(MADI_ERR_NULL, "%s: null pointer", what);
   if (epilogue != MADI_EPI_NONE && !bias) return fail(MADI_ERR_NULL, "%s: null bias", what);
   if (epilogue == MADI_EPI_BIAS_RES)
@@ -1805,18 +1830,24 @@ int q8_gemm(const char *what, const void *a, const void *qs, const void *scales,
     return fail(MADI_ERR_ALIGN, "%s: a/qs/scales/c/bias need 16-byte alignment", what);
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "%s: madi_init has not succeeded", what);
   if (int rc = deferred_before_read(a, (size_t)m * k * 2)) return rc;
-  if (int rc = deferred_before_write(c, (size_t)m * n * 2)) return rc;
+  if (seg.n == 0) {
+    if (int rc = deferred_before_write(c, (size_t)m * n * 2)) return rc;
+  } else {
+    for (int s = 0; s < kMaxSegs && s * seg.n < n; ++s)
+      if (int rc = deferred_before_write(seg.c[s], (size_t)m * seg.n * 2)) return rc;
+  }
   const f16 *A = static_cast<const f16 *>(a);
   const uint8_t *Q = static_cast<const uint8_t *>(qs);
   const f16 *S = static_cast<const f16 *>(scales);
   f16 *C = static_cast<f16 *>(c);
-  if (m <= 32) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k, where);
-  if (m <= 64) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  if (m <= 32) return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k, where, seg);
+  if (m <= 64) return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k, where, seg);
   // Where 128-row tiles would split K: the in-workgroup K split on 128 x 64
   // tiles where the shape suits it (fc2 at M = 1500), else 64-row tiles, which
   // halve the split count and the partial sums through memory (2 splits of
   // 40 chunks instead of 4 of 20).
   if (split_count(tile_count(m, n, 4), k / kChunkK) > 1) {
+    if (seg.n) return kSegUnsupported;
     if (const uint32_t cw = ks_chunks(m, n, k)) {
       switch (epilogue) {
       case MADI_EPI_NONE: return launch_ks<MADI_EPI_NONE>(A, Q, S, C, bias, m, n, k, cw);
@@ -1825,7 +1856,7 @@ int q8_gemm(const char *what, const void *a, const void *qs, const void *scales,
       default: return fail(MADI_ERR_ARG, "%s: unknown epilogue %d", what, epilogue);
       }
     }
-    return dispatch_epi<kSplitTile>(epilogue, A, Q, S, C, bias, m, n, k, where);
+    return dispatch_epi<kSplitTile>(epilogue, A, Q, S, C, bias, m, n, k, where, seg);
   }
   // Otherwise the lowest tiles whose count still fits one workgroup per CU:
   // a lower tile does less MFMA work per byte loaded (a 32-row tile takes
@@ -1842,15 +1873,17 @@ int q8_gemm(const char *what, const void *a, const void *qs, const void *scales,
   const bool narrow = narrow_ok(k);
   if (tile_count(m, n, 1) <= cus) {
     if (narrow && tile_count(m, n, 2, 1) <= cus)
-      return dispatch_epi<2, 1>(epilogue, A, Q, S, C, bias, m, n, k, where);
-    return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k, where);
+      return dispatch_epi<2, 1>(epilogue, A, Q, S, C, bias, m, n, k, where, seg);
+    return dispatch_epi<1>(epilogue, A, Q, S, C, bias, m, n, k, where, seg);
   }
   if (tile_count(m, n, 2) <= cus) {
     if (narrow && tile_count(m, n, 4, 1) <= cus)
-      return dispatch_epi<4, 1>(epilogue, A, Q, S, C, bias, m, n, k, where);
-    return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k, where);
+      return dispatch_epi<4, 1>(epilogue, A, Q, S, C, bias, m, n, k, where, seg);
+    return dispatch_epi<2>(epilogue, A, Q, S, C, bias, m, n, k, where, seg);
   }
-  if (tile_count(m, n, 3) <= cus) return dispatch_epi<3>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  if (tile_count(m, n, 3) <= cus)
+    return dispatch_epi<3>(epilogue, A, Q, S, C, bias, m, n, k, where, seg);
+  if (seg.n) return kSegUnsupported;
   // at least two rounds of 128-row tiles: the persistent tile loop
   if (persist_ok(m, n, k)) {
     switch (epilogue) {
@@ -1860,7 +1893,7 @@ int q8_gemm(const char *what, const void *a, const void *qs, const void *scales,
     default: return fail(MADI_ERR_ARG, "%s: unknown epilogue %d", what, epilogue);
     }
   }
-  return dispatch_epi<4>(epilogue, A, Q, S, C, bias, m, n, k, where);
+  return dispatch_epi<4>(epilogue, A, Q, S, C, bias, m, n, k, where, seg);
 }
 
 }  // namespace
@@ -1903,6 +1936,20 @@ int q8_gemm_f32io(const float *in, const void *qs, const void *scales, float *ou
       !loop_padded(chunks, splits))
     return launch_gemm<2, MADI_EPI_NONE, true, 1>(in, Q, S, out, nullptr, m, n, k, kWorkspace);
   return launch_gemm<2, MADI_EPI_NONE, true>(in, Q, S, out, nullptr, m, n, k, kWorkspace);
+}
+}  // namespace madi
+
+namespace madi {
+int q8_gemm_seg(const void *a, const void *qs, const void *scales, const OutSeg &seg, uint32_t m,
+                uint32_t n, uint32_t k, int epilogue) {
+  // every segment's output and bias meets madi_q8_gemm's own checks; the
+  // launch checks below are then made on segment 0's pointers
+  if (seg.n == 0 || n % seg.n || n / seg.n > (uint32_t)kMaxSegs) return kSegUnsupported;
+  for (uint32_t s = 0; s < n / seg.n; ++s)
+    if (!seg.c[s] || !aligned(seg.c[s], 16) || (epilogue != MADI_EPI_NONE && (!seg.b[s] || !aligned(seg.b[s], 16))))
+      return kSegUnsupported;
+  return q8_gemm("madi_q8_gemm", a, qs, scales, seg.c[0], epilogue != MADI_EPI_NONE ? seg.b[0] : nullptr,
+                 m, n, k, epilogue, kWorkspace, seg);
 }
 }  // namespace madi
 

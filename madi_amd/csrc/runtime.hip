@@ -212,17 +212,22 @@ extern "C" int madi_begin_command_buffer(void) {
 
 extern "C" int madi_commit_command_buffer(void) {
   if (!g_init) return fail(MADI_ERR_NOT_INIT, "madi_commit_command_buffer: not initialised");
+  if (int rc = group_flush()) return rc;
   return check_launch("madi_commit_command_buffer");
 }
 
 extern "C" int madi_sync(void) {
   if (!g_init) return fail(MADI_ERR_NOT_INIT, "madi_sync: madi_init has not succeeded");
+  if (int rc = group_flush()) return rc;
   hipError_t e = hipStreamSynchronize(g_stream);
   if (e != hipSuccess) return fail(MADI_ERR_SYNC, "madi_sync: %s", hipGetErrorString(e));
   return MADI_OK;
 }
 
 extern "C" int madi_set_stream(void *s) {
+  // work held for a later launch goes to the stream it was issued on
+  if (g_init)
+    if (int rc = group_flush()) return rc;
   g_stream = reinterpret_cast<hipStream_t>(s);
   return MADI_OK;
 }

@@ -124,6 +124,44 @@ def upload_q8(qs: np.ndarray, scales: np.ndarray, device="cuda") -> Q8:
     return Q8(dq.data_ptr(), ds.data_ptr(), (dq, ds))
 
 
+class _MadiBuf:
+    """A madi_alloc allocation, freed with madi_free when dropped."""
+
+    def __init__(self, nbytes: int):
+        self.p = lib().madi_alloc(nbytes)
+        if not self.p:
+            raise MadiError(-2, "madi_alloc", _last_error())
+
+    def __del__(self):
+        if getattr(self, "p", None):
+            try:
+                lib().madi_free(self.p)
+            except Exception:
+                pass
+            self.p = None
+
+
+def _last_error() -> str:
+    from ._lib import last_error
+    return last_error()
+
+
+def upload_q8_alloc(qs: np.ndarray, scales: np.ndarray) -> Q8:
+    """Load-time path as the engine's loader runs it: the weight in its own
+    madi_alloc allocation (mtl.alloc), repacked on the host and uploaded
+    (madi_upload).  A stacked q|k|v weight loaded this way is what the q|k|v
+    grouping recognises."""
+    tq, ts = repack_host(qs, scales)
+    bq, bs = _MadiBuf(tq.nbytes), _MadiBuf(ts.nbytes)
+    call("madi_upload", bq.p, tq.ctypes.data, tq.nbytes)
+    call("madi_upload", bs.p, ts.ctypes.data, ts.nbytes)
+    return Q8(bq.p, bs.p, (bq, bs))
+
+
+def set_gemm_grouping(on: bool) -> None:
+    call("madi_set_gemm_grouping", 1 if on else 0)
+
+
 def upload_q8_device_repack(qs: np.ndarray, scales: np.ndarray, device="cuda") -> Q8:
     """Load-time path: copy the natural rows to HBM, repack there (madi_q8_repack)."""
     import torch
@@ -284,7 +322,7 @@ def gemv_f16x(out, x16, w: Q8, n: int, k: int, bias=None, epilogue: int = EPI_NO
 __all__ = [
     "D", "MLP", "VOCAB", "ENC_SEQ", "NH", "Q8", "init", "sync", "getFunction", "materialize",
     "set_deferred_dequant", "forget", "repack_host", "unpack_host",
-    "upload_q8", "upload_q8_device_repack", "quantize", "fnv", "FNV_SEED", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias", "kM4", "kM4Bias", "kFlash", "matmulF16Batched",
+    "upload_q8", "upload_q8_alloc", "set_gemm_grouping", "upload_q8_device_repack", "quantize", "fnv", "FNV_SEED", "kDeq", "deqW16", "kGemmQ8", "kGemmQ8Bias", "kM4", "kM4Bias", "kFlash", "matmulF16Batched",
     "kGemvQ8", "kGemvQ8Bias", "kGemvQ8BiasEpi", "pproj", "proj", "kQkv", "kLogitGemv", "embLookup",
     "embLookupIndirect", "prefillEmbed", "gemv_f16x", "EPI_NONE", "EPI_BIAS", "EPI_BIAS_GELU",
     "EPI_BIAS_RES",

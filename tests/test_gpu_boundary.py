@@ -530,3 +530,79 @@ def test_smaller_kdeq_shortens_the_earlier_record(q):
     want2[2048:2064] = 7
     assert np.array_equal(got2, want2)
     wdq2.free()
+
+
+def test_qkv_slices_run_as_one_grouped_launch(q):
+    """encoder.zig:262-267 with the stacked q|k|v weight in its own madi_alloc
+    allocation (as the engine's loader makes it): the q GEMM is held (its
+    output untouched after the call), k joins, and v completes the group,
+    which runs as one stacked 1280 -> 3840 launch into the three blocks of
+    s.qkv.  The outputs equal, bit for bit, the three GEMMs launched one by
+    one (grouping off: the same MFMA order per output), and the oracle.  A
+    held group is launched by madi_sync, by a library read of a held output,
+    by a write of a held operand, and by a GEMM that does not join."""
+    say("q|k|v grouping")
+    rng = np.random.default_rng(267)
+    m = 1500
+    qkv_qs, qkv_sc = synth.q8_weight(rng, 3 * D, D)
+    w = q.upload_q8_alloc(qkv_qs, qkv_sc)
+    b = [dev(rng.standard_normal(D).astype(np.float32)) for _ in range(3)]
+    x = synth.activations(rng, m, D)
+    d_x = dev_f16(x)
+    wdq, wdq2 = sentinel(D * D), sentinel(D * D)
+    m4b = q.getFunction("m4_gemm_bias")
+
+    def issue(qkv, upto=3):
+        q.kDeq(wdq, w, D, D)
+        q.kM4Bias(m4b, d_x, wdq, qkv[0], b[0], m, D, D)
+        if upto > 1:
+            q.kDeq(wdq2, w.rows(D, D), D, D)
+            q.kM4Bias(m4b, d_x, wdq2, qkv[1], b[1], m, D, D)
+        if upto > 2:
+            q.kDeq(wdq, w.rows(2 * D, D), D, D)
+            q.kM4Bias(m4b, d_x, wdq, qkv[2], b[2], m, D, D)
+
+    grouped = sentinel(3 * m * D).view(3, m, D)
+    q.set_gemm_grouping(True)
+    # held: after the q call (and a device-wide wait outside the library) the
+    # q block is still the sentinel
+    issue(grouped, upto=1)
+    torch.cuda.synchronize()
+    assert np.all(grouped[0].cpu().numpy().view(np.uint16) == NAN16)
+    issue(grouped, upto=3)   # q again (replaces nothing: joins are by slice), k, v
+    q.sync()
+    g = grouped.cpu().numpy().view(np.uint16)
+    q.set_gemm_grouping(False)
+    single = sentinel(3 * m * D).view(3, m, D)
+    issue(single)
+    q.sync()
+    q.set_gemm_grouping(True)
+    s_ = single.cpu().numpy().view(np.uint16)
+    assert np.array_equal(g, s_)
+    for i in range(3):
+        check_gemm(grouped[i], x, qkv_qs[i * D:(i + 1) * D], qkv_sc[i * D:(i + 1) * D],
+                   b[i].cpu().numpy(), O.EPI_BIAS)
+    assert np.all(wdq.cpu().numpy().view(np.uint16) == NAN16)
+
+    # what launches a held group
+    def held_then(action, upto=1):
+        out = sentinel(3 * m * D).view(3, m, D)
+        issue(out, upto=upto)
+        action(out)
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().view(np.uint16)
+        assert np.array_equal(got[:upto], s_[:upto]), action
+        q.sync()
+    held_then(lambda out: q.sync())
+    held_then(lambda out: _lib.call("madi_download", np.empty(8, np.uint16).ctypes.data,
+                                    out[1].data_ptr(), 16), upto=2)      # a read of k
+    o_qs, o_sc = synth.q8_weight(rng, D, D)
+    o_w = q.upload_q8(o_qs, o_sc)
+    mo = sentinel(m * D)
+
+    def out_proj(out):  # the next kDeq + kM4 pair (out-proj): does not join
+        q.kDeq(wdq, o_w, D, D)
+        q.kM4("m4_gemm_nn", d_x, wdq, mo, m, D, D)
+    held_then(out_proj, upto=2)
+    held_then(lambda out: _lib.call("madi_upload", d_x.data_ptr(),
+                                    np.ascontiguousarray(x[:4]).ctypes.data, 16))  # a write of x
