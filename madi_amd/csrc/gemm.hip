@@ -750,7 +750,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   const uint32_t first = (x * W) >> 3, run = (((x + 1) * W) >> 3) - first;
   if ((L >> 3) >= run) return;
   const uint32_t item = first + (L >> 3);
-  const uint32_t bid = item / splits, split = item - bid * splits;
+  // launches that never split K (the m-tile-major tail, the f16 128-column
+  // tiles: the host checks) skip the division
+  constexpr bool kUnsplit = TAIL || (PW == 1 && !F32);
+  const uint32_t bid = kUnsplit ? item : item / splits, split = kUnsplit ? 0u : item - bid * splits;
   const uint32_t tile = bid;
   const uint32_t group_m = tiles_m < 6 ? tiles_m : 6;
   const uint32_t per_group = group_m * tiles_n;
@@ -817,10 +820,18 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     RawWT<PW> &rw = j == -4 ? r0 : j == -3 ? r1 : j == -2 ? r2 : r3;
 #pragma unroll
     for (int st = 0; st < 4; ++st)
-      issue_loads<MT, F32, kSel>(st, slot, (uint32_t)(j + DA), rw, (uint32_t)(j + WD), p, lane);
+      // unpadded loops have at least eight chunks per split: all four live
+      issue_loads<MT, F32, PADDED ? kSel : kLive>(st, slot, (uint32_t)(j + DA), rw,
+                                                 (uint32_t)(j + WD), p, lane);
   }
   // chunk 0's weights and the A stages of chunks 0 and 1 (chunk 0 reads
-  // chunk 1's stage without a barrier of its own), then chunk 0's fragments
+  // chunk 1's stage without a barrier of its own), then chunk 0's fragments.
+  // The wave reaches this wait only once the CU's load pipe has accepted all
+  // four chunks' loads (128 KiB per CU at ~64 bytes per cycle: ~2000 of the
+  // ~3400 cycles before the first MFMA, measured with per-wave stamps);
+  // waiting after the first two chunks' loads instead (the rest issued after
+  // the barrier) measured no faster, since the wave still issues the rest
+  // before its first MFMA.
   wait_then_barrier<G::kVmPrologue>();
   wait_weights<G::kVmPrologue>(r0);
   f16x8 w[PW][4];
