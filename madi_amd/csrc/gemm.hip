@@ -213,7 +213,10 @@ __device__ inline void dma_range(desc_t wa, const Plan<MT, F32, PW> &p, uint32_t
 // lie past the end: they issue nothing.  A load whose result is never used
 // must not be issued at all: the compiler sees the asm write its registers at
 // once and reuses them while the load is still in flight.
-enum Prefetch { kSel = 0, kLive = 1, kLast0 = 2, kLast1 = 3, kLast2 = 4, kLast3 = 5, kLiveE = 6 };
+enum Prefetch {
+  kSel = 0, kLive = 1, kLast0 = 2, kLast1 = 3, kLast2 = 4, kLast3 = 5, kLiveE = 6,
+  kRamp0 = 7, kRamp1 = 8
+};
 
 // The vmcnt counts of a chunk's two waits: `raw` at its start (chunk c+1's
 // weights, issued in chunk c+1-WD, have landed once only the loads issued
@@ -224,16 +227,26 @@ enum Prefetch { kSel = 0, kLive = 1, kLast0 = 2, kLast1 = 3, kLast2 = 4, kLast3 
 // prologue loads are followed by E other vector-memory issues (the previous
 // tile's epilogue) before the K loop: the waits whose targets lie in the
 // prologue (chunks 0-2's weights, chunk 3's A stage) allow E more.
+// kRamp0 / kRamp1: chunks 0 and 1 of a ramped start (the prologue issues
+// chunks 0 and 1 only; chunk 0 issues chunks 2 and 3, chunk 1 chunks 4 and
+// 5, in the same global order as the steady state): chunk 0 waits for chunk
+// 1's weights with nothing issued after them, chunk 1 for chunk 2's with
+// chunk 3's loads after them, and chunk 1's barrier for chunk 3's A stage
+// with chunk 3's weights, chunk 4's loads and chunk 5's A stage and first
+// weight unit after it.
 template <int MT, bool F32, int PF, int E = 0, int PW = 2>
 struct Waits {
   using G = Geometry<MT, F32, PW>;
   static constexpr int raw = PF == kLiveE ? G::kVmRaw + E
                            : PF == kLast1 ? G::kPerChunk
                            : (PF >= kLast2 && PF <= kLast3) ? 0
+                           : PF == kRamp0 ? 0
+                           : PF == kRamp1 ? G::kPerChunk
                                           : G::kVmRaw;
   static constexpr int a = PF == kLiveE ? G::kVmA + E
                          : PF == kLast1 ? G::LW
                          : PF == kLast3 ? 0
+                         : PF == kRamp1 ? G::LW + G::kPerChunk + G::LA + 1
                                         : G::kVmA;
   static_assert(raw >= 0 && raw < 64 && a >= 0 && a < 64, "vmcnt range");
 };
@@ -366,11 +379,31 @@ __device__ inline void schedule_step() {
 // and `nxt` receives chunk c+1's weights (loaded WD-1 chunks ago; waited for
 // here).  `ld` (the same register set as `cur`, free after step 0) receives
 // chunk c+WD's weights.
+// The ramped start's loads for k-step s of chunk c (0 or 1): chunks 2c + 2
+// and 2c + 3, the first into register set `la` and A stage 2c + 2, the
+// second into `lb` and stage 2c + 3; k-steps 0-1 issue the first chunk's
+// plan (A stage, then weights), k-steps 2-3 the second's.
+template <int MT, bool F32, int PW>
+__device__ inline void ramp_loads(int s, uint8_t *smem, uint32_t c, const Plan<MT, F32, PW> &p,
+                                  uint32_t lane, RawWT<PW> &la, RawWT<PW> &lb) {
+  using G = Geometry<MT, F32, PW>;
+  const uint32_t c0 = 2 * c + 2, c1 = 2 * c + 3;
+  if (s < 2) {
+    uint8_t *slot = smem + (c0 % NA) * G::kStage;
+    issue_loads<MT, F32, kLive>(2 * s, slot, c0, la, c0, p, lane);
+    issue_loads<MT, F32, kLive>(2 * s + 1, slot, c0, la, c0, p, lane);
+  } else {
+    uint8_t *slot = smem + (c1 % NA) * G::kStage;
+    issue_loads<MT, F32, kLive>(2 * (s - 2), slot, c1, lb, c1, p, lane);
+    issue_loads<MT, F32, kLive>(2 * (s - 2) + 1, slot, c1, lb, c1, p, lane);
+  }
+}
+
 template <int MT, bool F32, int PF, bool ODD, int E = 0, int PW = 2>
 __device__ inline void chunk(uint8_t *smem, const Plan<MT, F32, PW> &p, uint32_t c, uint32_t lane,
                              uint32_t h, uint32_t r, f32x16 (&acc)[PW][MT], f16x8 (&w)[PW][4],
                              typename AFrag<F32>::T (&af)[MT], const RawWT<PW> &cur,
-                             RawWT<PW> &nxt, RawWT<PW> &ld) {
+                             RawWT<PW> &nxt, RawWT<PW> &ld, RawWT<PW> &ld2) {
   using G = Geometry<MT, F32, PW>;
   using WT = Waits<MT, F32, PF, E, PW>;
   const uint8_t *At = smem + (c % NA) * G::kStage;
@@ -409,7 +442,14 @@ __device__ inline void chunk(uint8_t *smem, const Plan<MT, F32, PW> &p, uint32_t
       // next value is chunk c's own step-3 fragment at step 0, else chunk c+1's
       w[t][(s + 3) & 3] = dequant_frag(s == 0 ? cur : nxt, t, (s + 3) & 3);
     }
-    issue_loads<MT, F32, PF == kLiveE ? kLive : PF>(s, Af, c + DA, ld, c + WD, p, lane);
+    if constexpr (PF == kRamp0 || PF == kRamp1) {
+      // two chunks' loads over the four k-steps, in global order (chunk 0:
+      // chunks 2 and 3 into register sets `ld`, `ld2`; chunk 1: chunks 4
+      // and 5)
+      ramp_loads<MT, F32, PW>(s, smem, c, p, lane, ld, ld2);
+    } else {
+      issue_loads<MT, F32, PF == kLiveE ? kLive : PF>(s, Af, c + DA, ld, c + WD, p, lane);
+    }
 #pragma unroll
     for (int i = 0; i < MT; ++i) af[i] = an[i];
     schedule_step<MT, F32, PW>();
@@ -814,8 +854,17 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   RawWT<PW> r0, r1, r2, r3;
   static_assert(WD == 4 && DA == 4, "the loop below rotates four weight register sets");
   static_assert(NA >= DA + 2, "an A stage is refilled only after the barrier that retires it");
+  // Ramped start (the m-tile-major tail's launches, at least twelve chunks:
+  // the host checks): the prologue issues chunks 0 and 1 only, and chunks 0
+  // and 1 issue chunks 2-5 among their MFMAs, in the steady state's global
+  // order, so every later wait keeps its count.  The CU's load pipe accepts
+  // ~64 bytes per cycle, so the four-chunk prologue (128 KiB per CU) held the
+  // first MFMA back ~2000 cycles (per-wave stamps); waiting after two
+  // chunks' loads with the rest issued before the first MFMA measured no
+  // faster.
+  constexpr bool kRamp = TAIL;
 #pragma unroll
-  for (int j = -4; j < 0; ++j) {
+  for (int j = -4; j < (kRamp ? -2 : 0); ++j) {
     uint8_t *slot = smem + (uint32_t)(j + DA) * G::kStage;
     RawWT<PW> &rw = j == -4 ? r0 : j == -3 ? r1 : j == -2 ? r2 : r3;
 #pragma unroll
@@ -825,15 +874,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
                                                  (uint32_t)(j + WD), p, lane);
   }
   // chunk 0's weights and the A stages of chunks 0 and 1 (chunk 0 reads
-  // chunk 1's stage without a barrier of its own), then chunk 0's fragments.
-  // The wave reaches this wait only once the CU's load pipe has accepted all
-  // four chunks' loads (128 KiB per CU at ~64 bytes per cycle: ~2000 of the
-  // ~3400 cycles before the first MFMA, measured with per-wave stamps);
-  // waiting after the first two chunks' loads instead (the rest issued after
-  // the barrier) measured no faster, since the wave still issues the rest
-  // before its first MFMA.
-  wait_then_barrier<G::kVmPrologue>();
-  wait_weights<G::kVmPrologue>(r0);
+  // chunk 1's stage without a barrier of its own), then chunk 0's fragments
+  constexpr int kVmStart = kRamp ? G::LW : G::kVmPrologue;
+  wait_then_barrier<kVmStart>();
+  wait_weights<kVmStart>(r0);
   f16x8 w[PW][4];
   typename AFrag<F32>::T af[MT];
 #pragma unroll
@@ -850,21 +894,28 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
   if constexpr (PADDED) {
     const uint32_t cpad = (nchunks + WD - 1) / WD * WD;
     for (uint32_t c = 0; c < cpad; c += 4) {
-      chunk<MT, F32, kSel, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-      chunk<MT, F32, kSel, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-      chunk<MT, F32, kSel, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-      chunk<MT, F32, kSel, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+      chunk<MT, F32, kSel, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0, r0);
+      chunk<MT, F32, kSel, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1, r1);
+      chunk<MT, F32, kSel, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2, r2);
+      chunk<MT, F32, kSel, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3, r3);
     }
   } else {
     // at least two trips (the host checks): the loop is never skipped, so the
     // prologue's registers reach the last trip only through it and need no
     // copies on a path around it
     uint32_t c = 0;
+    if constexpr (kRamp) {
+      chunk<MT, F32, kRamp0, false>(smem, p, 0, lane, h, r, acc, w, af, r0, r1, r2, r3);
+      chunk<MT, F32, kRamp1, true>(smem, p, 1, lane, h, r, acc, w, af, r1, r2, r0, r1);
+      chunk<MT, F32, kLive, false>(smem, p, 2, lane, h, r, acc, w, af, r2, r3, r2, r2);
+      chunk<MT, F32, kLive, true>(smem, p, 3, lane, h, r, acc, w, af, r3, r0, r3, r3);
+      c = 4;
+    }
     do {
-      chunk<MT, F32, kLive, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-      chunk<MT, F32, kLive, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-      chunk<MT, F32, kLive, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-      chunk<MT, F32, kLive, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+      chunk<MT, F32, kLive, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0, r0);
+      chunk<MT, F32, kLive, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1, r1);
+      chunk<MT, F32, kLive, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2, r2);
+      chunk<MT, F32, kLive, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3, r3);
       c += 4;
     } while (c + 2 * WD <= nchunks);
     if constexpr (TAIL) {
@@ -874,10 +925,10 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
                     ot.b, M, ot.n, m0, ot.p0, ot.np);
       return;
     } else {
-      chunk<MT, F32, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-      chunk<MT, F32, kLast1, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-      chunk<MT, F32, kLast2, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-      chunk<MT, F32, kLast3, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+      chunk<MT, F32, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0, r0);
+      chunk<MT, F32, kLast1, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1, r1);
+      chunk<MT, F32, kLast2, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2, r2);
+      chunk<MT, F32, kLast3, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3, r3);
     }
   }
 
@@ -1204,22 +1255,22 @@ __global__ __launch_bounds__(256) void q8_gemm_persist_kernel(
 
     // K loop: first trip (targets before it in the prologue), live trips, the
     // peeled last trip; nchunks a multiple of four and at least 12
-    chunk<MT, false, kLiveE, false, P::kEpi>(smem, p, 0, lane, h, r, acc, w, af, r0, r1, r0);
-    chunk<MT, false, kLiveE, true, P::kEpi>(smem, p, 1, lane, h, r, acc, w, af, r1, r2, r1);
-    chunk<MT, false, kLiveE, false, P::kEpi>(smem, p, 2, lane, h, r, acc, w, af, r2, r3, r2);
-    chunk<MT, false, kLive, true>(smem, p, 3, lane, h, r, acc, w, af, r3, r0, r3);
+    chunk<MT, false, kLiveE, false, P::kEpi>(smem, p, 0, lane, h, r, acc, w, af, r0, r1, r0, r0);
+    chunk<MT, false, kLiveE, true, P::kEpi>(smem, p, 1, lane, h, r, acc, w, af, r1, r2, r1, r1);
+    chunk<MT, false, kLiveE, false, P::kEpi>(smem, p, 2, lane, h, r, acc, w, af, r2, r3, r2, r2);
+    chunk<MT, false, kLive, true>(smem, p, 3, lane, h, r, acc, w, af, r3, r0, r3, r3);
     uint32_t c = 4;
     do {
-      chunk<MT, false, kLive, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-      chunk<MT, false, kLive, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-      chunk<MT, false, kLive, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-      chunk<MT, false, kLive, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+      chunk<MT, false, kLive, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0, r0);
+      chunk<MT, false, kLive, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1, r1);
+      chunk<MT, false, kLive, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2, r2);
+      chunk<MT, false, kLive, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3, r3);
       c += 4;
     } while (c + 2 * WD <= nchunks);
-    chunk<MT, false, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0);
-    chunk<MT, false, kLast1, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1);
-    chunk<MT, false, kLast2, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2);
-    chunk<MT, false, kLast3, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3);
+    chunk<MT, false, kLast0, false>(smem, p, c + 0, lane, h, r, acc, w, af, r0, r1, r0, r0);
+    chunk<MT, false, kLast1, true>(smem, p, c + 1, lane, h, r, acc, w, af, r1, r2, r1, r1);
+    chunk<MT, false, kLast2, false>(smem, p, c + 2, lane, h, r, acc, w, af, r2, r3, r2, r2);
+    chunk<MT, false, kLast3, true>(smem, p, c + 3, lane, h, r, acc, w, af, r3, r0, r3, r3);
     drain(r0, r1, r2, r3);
     wait_then_barrier<0>();  // every wave is done with the ring
 
@@ -1742,9 +1793,10 @@ int resolve_scratch(uint8_t **out) {
 
 // The m-tile-major tail serves unpadded, unsplit f16 launches of two or more
 // m-tiles (MADI_GEMM_TAIL=0 selects the chunk-by-chunk last trip instead).
-bool use_tail(uint32_t splits) {
+bool use_tail(uint32_t splits, uint32_t chunks) {
   const char *e = getenv("MADI_GEMM_TAIL");
-  return splits == 1 && !(e && e[0] == '0');
+  // the ramped first trip, then at least one steady trip, then the tail
+  return splits == 1 && chunks >= 12 && !(e && e[0] == '0');
 }
 
 // Where a launch keeps its split-K partials and counters.
@@ -1797,7 +1849,7 @@ int launch_gemm(const void *A, const uint8_t *qs, const f16 *sc, void *C, const 
   } else if (padded)
     go(q8_gemm_kernel<MT, EPI, true, F32>);
   else if constexpr (!F32 && MT >= 2) {
-    if (use_tail(splits))
+    if (use_tail(splits, chunks))
       go(q8_gemm_kernel<MT, EPI, false, false, true>);
     else
       go(q8_gemm_kernel<MT, EPI, false, false>);
