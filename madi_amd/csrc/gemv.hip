@@ -9,14 +9,16 @@
 // one contiguous KiB (16 bytes per lane, lane (h, r) receiving 16 weights of
 // row r in quantisation block h), issued as a buffer load with the
 // panel/chunk offset in an SGPR.  Each wave streams its K range through a
-// two-chunk window (use chunk c, refill with chunk c+2).  The kernel keeps to
-// 48 - 65 VGPRs (seven waves per SIMD), so every four-wave workgroup of the
-// 51866-row vocab matrix (1621 panels, seven per CU) is resident from the
-// start.
+// two-chunk window (use chunk c, refill with chunk c+2).  The four-wave
+// instances keep to 48 - 65 VGPRs (seven waves per SIMD), so every workgroup
+// of the 51866-row vocab matrix (1621 panels, seven per CU) is resident from
+// the start; the sixteen-wave ones (four waves per SIMD) take up to 94.
 //
 // The activation vector is loaded next to the first weight window (before
 // it for the narrow matrices, after it for the vocab), staged once per
-// workgroup in LDS and read back as broadcast 128-bit LDS loads.  v_perm_b32
+// workgroup in LDS and read back as broadcast 128-bit LDS loads, ahead of
+// the weights they meet (the narrow matrices' first window while its weights
+// are in flight; the vocab's fp32 vector one 16-value unit ahead).  v_perm_b32
 // turns two stored bytes u = q + 128 into the fp16 pair 1024 + u and one
 // packed subtract of 1152 leaves the exact fp16 pair (q0, q1); fp16
 // activations accumulate x * q with v_dot2_f32_f16 (exact products, fp32
@@ -128,15 +130,52 @@ __device__ inline float unit_dot(const u32x4 &w, const float *x32, float part) {
   return part;
 }
 
-// acc += scale * (sum_k x[k] q[k]) over the lane's quantisation block of chunk c
+// One 16-weight unit's fp32 activations in registers, and its sum against
+// them (the same FMA order as unit_dot).
+struct XUnit {
+  f32x4 v[4];
+};
+__device__ inline XUnit read_unit(const float *x32) {
+  XUnit u;
+#pragma unroll
+  for (int d = 0; d < 4; ++d) u.v[d] = *reinterpret_cast<const f32x4 *>(x32 + 4 * d);
+  return u;
+}
+__device__ inline float unit_dot(const u32x4 &w, const XUnit &x, float part) {
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const f16x2 q01 = q_pair(wd[d], kSelLo), q23 = q_pair(wd[d], kSelHi);
+    part = __builtin_fmaf(x.v[d].x, (float)q01.x, part);
+    part = __builtin_fmaf(x.v[d].y, (float)q01.y, part);
+    part = __builtin_fmaf(x.v[d].z, (float)q23.x, part);
+    part = __builtin_fmaf(x.v[d].w, (float)q23.y, part);
+  }
+  return part;
+}
+
+// acc += scale * (sum_k x[k] q[k]) over the lane's quantisation block, its
+// 32 activations at xp (LDS, or registers)
+template <typename XT>
+__device__ inline void accumulate_x(const ChunkW &b, const XT *xp, float &acc) {
+  float part = unit_dot(b.w[0], xp, 0.0f);
+  part = unit_dot(b.w[1], xp + 16, part);
+  acc = __builtin_fmaf(part, (float)__builtin_bit_cast(f16, (uint16_t)b.s), acc);
+}
+// the same over the lane's block of chunk c, x in LDS
 template <typename XT>
 __device__ inline void accumulate(const ChunkW &b, uint32_t c, const XT *xs, uint32_t h,
                                   float &acc) {
-  const uint32_t k0 = c * kChunkK + h * 32;  // the lane's 32-wide block
-  float part = unit_dot(b.w[0], xs + k0, 0.0f);
-  part = unit_dot(b.w[1], xs + k0 + 16, part);
-  acc = __builtin_fmaf(part, (float)__builtin_bit_cast(f16, (uint16_t)b.s), acc);
+  accumulate_x(b, xs + c * kChunkK + h * 32, acc);
 }
+
+template <typename XT>
+constexpr bool kBlockF32 = sizeof(XT) == 4;
+
+// Narrow matrices: sixteen waves of one panel, four per SIMD, so up to 128
+// VGPRs each (the first window's activations are held in registers, below).
+template <int KW>
+constexpr int kWavesPerEu = KW == kWavesNarrow ? 4 : 7;
 
 template <typename XT, int MODE, int KW>
 //
@@ -144,7 +183,7 @@ template <typename XT, int MODE, int KW>
 // kernel first needs them, so the leading ones arrive preloaded in SGPRs, and
 // the set-up has no integer division: split s covers chunks [s * cper +
 // min(s, crem), + cper + (s < crem)).
-__global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(7))) void q8_gemv_kernel(
+__global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(kWavesPerEu<KW>))) void q8_gemv_kernel(
     const uint8_t *qs, const f16 *sc, const void *x, uint32_t n, uint32_t k, uint32_t cper,
     uint32_t crem, float *out, const float *bias, float *wsp, uint32_t *cnt, const float *qb,
     const float *vb, float *kc, float *vc, const uint32_t *pos) {
@@ -236,8 +275,66 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(7))) vo
   // stream the range through the kWin-chunk window: use chunk c, refill its
   // registers with chunk c + kWin
   float acc = 0.0f;
+  uint32_t cfirst = c0;
+  if constexpr (KW == kWavesNarrow) {
+    // Narrow matrices (one or two chunks per wave): the first window's
+    // activations are read from LDS now, while its weights are still in
+    // flight, instead of after they land, when all sixteen waves would queue
+    // at the LDS at once.
+    if (c0 < c1) {
+      XT xf[kWin][32];
+#pragma unroll
+      for (int k = 0; k < kWin; ++k) {
+        const uint32_t cc = c0 + k < c1 ? c0 + k : c1 - 1;
+#pragma unroll
+        for (int i = 0; i < 32; ++i) xf[k][i] = xs[cc * kChunkK + h * 32 + i];
+      }
+      // the reads stay ahead of the first wait for the weights
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int k = 0; k < kWin; ++k) {
+        accumulate_x<XT>(win[k], xf[k], acc);
+        const uint32_t cn = c0 + k + kWin;
+        const bool in = cn < c1;
+        load_chunk(win[k], in ? wq : wz, in ? ws : wz, K, cn, p, R, w_voff, s_voff);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      cfirst = c0 + kWin;
+    }
+  }
+  if constexpr (KW == kWaves && kBlockF32<XT>) {
+    // The vocab matrix with fp32 activations: each unit's activations are
+    // read from LDS one unit ahead of their use (the next chunk's first unit
+    // during this chunk's second), so the LDS latency passes under the
+    // arithmetic; a whole chunk ahead would not fit the 72 VGPRs that keep
+    // seven waves per SIMD.
+    const float *xf = reinterpret_cast<const float *>(xs) + h * 32;
+    XUnit xa = read_unit(xf + (c0 < c1 ? c0 : 0) * kChunkK);
 #pragma unroll 1
-  for (uint32_t c = c0; c < c1; c += kWin) {
+    for (uint32_t c = c0; c < c1; c += kWin) {
+#pragma unroll
+      for (int k = 0; k < kWin; ++k) {
+        const uint32_t cc = c + k < c1 ? c + k : c1 - 1;
+        const uint32_t cx = c + k + 1 < c1 ? c + k + 1 : c1 - 1;  // the next slot's chunk
+        // each read is issued before the arithmetic that precedes its use
+        const XUnit xb = read_unit(xf + cc * kChunkK + 16);
+        __builtin_amdgcn_sched_barrier(0);
+        float part = unit_dot(win[k].w[0], xa, 0.0f);
+        __builtin_amdgcn_sched_barrier(0);
+        xa = read_unit(xf + cx * kChunkK);
+        __builtin_amdgcn_sched_barrier(0);
+        part = unit_dot(win[k].w[1], xb, part);
+        acc = __builtin_fmaf(part, (float)__builtin_bit_cast(f16, (uint16_t)win[k].s), acc);
+        const uint32_t cn = c + k + kWin;
+        const bool in = cn < c1;
+        load_chunk(win[k], in ? wq : wz, in ? ws : wz, K, cn, p, R, w_voff, s_voff);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    cfirst = c1;
+  }
+#pragma unroll 1
+  for (uint32_t c = cfirst; c < c1; c += kWin) {
 #pragma unroll
     for (int k = 0; k < kWin; ++k) {
       // a chunk past the range (zeros, scale 0) reads the x of the range's
