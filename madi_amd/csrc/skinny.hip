@@ -27,8 +27,10 @@
 // zeros (outside the buffer resource).  The projections of a decode step are
 // small (1.6 - 6.5 MB of weights), so their time is load latency: each wave
 // keeps WIN chunks in flight, enough that the K range of most waves is one
-// round of loads; the K partial tiles meet in LDS and four waves store one
-// quarter each.
+// round of loads; the single-panel f32 launches load that whole first window's
+// activations ahead of its weights and stage them while the weights are in
+// flight.  The K partial tiles meet in LDS and four waves store one quarter
+// each.
 #include "common.h"
 
 using namespace madi;
@@ -69,25 +71,34 @@ struct Chunk {
 };
 
 template <int P, int XR, bool H>
-__device__ inline void load_chunk(Chunk<P, XR, H> &b, const Plan<P> &pl, uint32_t c) {
+__device__ inline void load_weights(Chunk<P, XR, H> &b, const Plan<P> &pl, rsrc_t wq, rsrc_t ws,
+                                    uint32_t c) {
 #pragma unroll
   for (int t = 0; t < P; ++t) {
     const uint32_t so = (uint32_t)panel_chunk_qs(pl.K, pl.p[t], pl.R[t], c);
-    b.w[t][0] = __builtin_amdgcn_raw_buffer_load_b128(pl.wq, pl.w_voff[t], so, 0);
-    b.w[t][1] = __builtin_amdgcn_raw_buffer_load_b128(pl.wq, pl.w_voff[t] + 2 * pl.R[t] * 16, so, 0);
+    b.w[t][0] = __builtin_amdgcn_raw_buffer_load_b128(wq, pl.w_voff[t], so, 0);
+    b.w[t][1] = __builtin_amdgcn_raw_buffer_load_b128(wq, pl.w_voff[t] + 2 * pl.R[t] * 16, so, 0);
     b.s[t] = __builtin_amdgcn_raw_buffer_load_b16(
-        pl.ws, pl.s_voff[t], (uint32_t)panel_chunk_sc(pl.K, pl.p[t], pl.R[t], c) * 2, 0);
+        ws, pl.s_voff[t], (uint32_t)panel_chunk_sc(pl.K, pl.p[t], pl.R[t], c) * 2, 0);
   }
+}
+template <int P, int XR, bool H>
+__device__ inline void load_acts(Chunk<P, XR, H> &b, const Plan<P> &pl, rsrc_t xr, uint32_t c) {
   if constexpr (H) {
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      b.xh[s] = __builtin_amdgcn_raw_buffer_load_b128(pl.xr, pl.x_voff, c * kChunkK * 2 + s * 16, 0);
+      b.xh[s] = __builtin_amdgcn_raw_buffer_load_b128(xr, pl.x_voff, c * kChunkK * 2 + s * 16, 0);
   } else {
 #pragma unroll
     for (int i = 0; i < XR / 4; ++i)
       b.x[i] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(pl.xr, pl.x_voff + i * 16 * pl.K, c * kChunkK * 4, 0));
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, pl.x_voff + i * 16 * pl.K, c * kChunkK * 4, 0));
   }
+}
+template <int P, int XR, bool H>
+__device__ inline void load_chunk(Chunk<P, XR, H> &b, const Plan<P> &pl, uint32_t c) {
+  load_weights(b, pl, pl.wq, pl.ws, c);
+  load_acts(b, pl, pl.xr, c);
 }
 
 // The wave's activation tile of one chunk in LDS: 32 rows x 64 f16, 128 bytes
@@ -98,28 +109,38 @@ __device__ inline uint32_t x_piece(uint32_t row, uint32_t j) {
   return row * 128 + ((j ^ ((row >> 1) & 7)) * 16);
 }
 
-// acc[t] += W_t(chunk) . X(chunk)^T over the four k-steps; step s uses half
-// (s & 1) of weight unit s >> 1 and activation piece 4h + s of row c.
+// f32 activations of a chunk -> f16 (round to nearest even, the kCvt32
+// staging) into the wave's LDS tile, 8 bytes per piece
 template <int P, int XR, bool H>
-__device__ inline void accumulate(const Chunk<P, XR, H> &b, uint8_t *xt, uint32_t lane,
-                                  f32x16 (&acc)[P]) {
-  const uint32_t h = lane >> 5, c = lane & 31;
-  // stage: f32 -> f16 (round to nearest even, the kCvt32 staging), 8 bytes per piece
-  if constexpr (!H) {
+__device__ inline void stage_acts(const Chunk<P, XR, H> &b, uint8_t *xt, uint32_t lane) {
 #pragma unroll
-    for (int i = 0; i < XR / 4; ++i) {
-      const uint32_t row = 4 * i + (lane >> 4), k4 = lane & 15;  // floats 4*k4 .. +3
-      const f16x4 v = {(f16)b.x[i].x, (f16)b.x[i].y, (f16)b.x[i].z, (f16)b.x[i].w};
-      *reinterpret_cast<f16x4 *>(xt + x_piece(row, k4 >> 1) + (k4 & 1) * 8) = v;
-    }
+  for (int i = 0; i < XR / 4; ++i) {
+    const uint32_t row = 4 * i + (lane >> 4), k4 = lane & 15;  // floats 4*k4 .. +3
+    const f16x4 v = {(f16)b.x[i].x, (f16)b.x[i].y, (f16)b.x[i].z, (f16)b.x[i].w};
+    *reinterpret_cast<f16x4 *>(xt + x_piece(row, k4 >> 1) + (k4 & 1) * 8) = v;
   }
+}
+
+// The four k-steps' activation fragments of a staged chunk: piece 4h + s of
+// row c (zeros for columns c >= XR)
+template <int XR>
+__device__ inline void read_frags(const uint8_t *xt, uint32_t lane, f16x8 (&xf)[4]) {
+  const uint32_t h = lane >> 5, c = lane & 31;
 #pragma unroll
   for (int s = 0; s < 4; ++s) {
-    f16x8 xf = {};
-    if constexpr (H)
-      xf = __builtin_bit_cast(f16x8, b.xh[s]);
-    else if (XR == 32 || c < XR)
-      xf = *reinterpret_cast<const f16x8 *>(xt + x_piece(c, 4 * h + s));
+    xf[s] = (f16x8){};
+    if (XR == 32 || c < XR) xf[s] = *reinterpret_cast<const f16x8 *>(xt + x_piece(c, 4 * h + s));
+  }
+}
+
+// acc[t] += W_t(chunk) . X(chunk)^T over the four k-steps; step s uses half
+// (s & 1) of weight unit s >> 1 and activation fragment s.
+template <int P, int XR, bool H>
+__device__ inline void mfma_chunk(const Chunk<P, XR, H> &b, const f16x8 (&xfr)[4],
+                                  f32x16 (&acc)[P]) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const f16x8 xf = xfr[s];
 #pragma unroll
     for (int t = 0; t < P; ++t) {
       const f16x2 s2 = {__builtin_bit_cast(f16, (uint16_t)b.s[t]),
@@ -134,12 +155,33 @@ __device__ inline void accumulate(const Chunk<P, XR, H> &b, uint8_t *xt, uint32_
   }
 }
 
+// One chunk: stage (f32 activations), read the fragments, MFMAs.
+template <int P, int XR, bool H>
+__device__ inline void accumulate(const Chunk<P, XR, H> &b, uint8_t *xt, uint32_t lane,
+                                  f32x16 (&acc)[P]) {
+  f16x8 xf[4];
+  if constexpr (H) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) xf[s] = __builtin_bit_cast(f16x8, b.xh[s]);
+  } else {
+    stage_acts(b, xt, lane);
+    read_frags<XR>(xt, lane, xf);
+  }
+  mfma_chunk(b, xf, acc);
+}
+
 
 // LDS: the waves' activation tiles (XR rows x 128 bytes) during the K loop,
 // then the partial sums of the reduction
-template <int P, int KW, int XR>
+// The single-panel f32 launches stage their whole first window at once: one
+// tile per window slot.
+template <int P, int KW, bool H>
+constexpr bool kStageWindow = P == 1 && KW == 8 && !H;
+
+template <int P, int KW, int XR, int WIN, bool H>
 constexpr int skinny_lds() {
-  return (KW * XR * 128 > KW * P * 4 * 64 * 16) ? KW * XR * 128 : KW * P * 4 * 64 * 16;
+  constexpr int tiles = KW * XR * 128 * (kStageWindow<P, KW, H> ? WIN : 1);
+  return tiles > KW * P * 4 * 64 * 16 ? tiles : KW * P * 4 * 64 * 16;
 }
 
 // P panels per workgroup, KW waves splitting K, XR activation rows loaded per
@@ -157,7 +199,7 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 
     const uint8_t *__restrict__ qs, const f16 *__restrict__ sc, const void *__restrict__ x,
     uint32_t M, uint32_t N, uint32_t K, uint32_t cper, uint32_t crem, uint32_t groups,
     void *__restrict__ out, f32x4 *ws, uint32_t *cnt) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[skinny_lds<P, KW, XR>()];
+  __shared__ __attribute__((aligned(16))) uint8_t smem[skinny_lds<P, KW, XR, WIN, H>()];
 
   // Consecutive workgroups go to different XCDs (round-robin, x fastest).
   // The grid's x extent is a multiple of 8, so every slice and K split of
@@ -198,16 +240,47 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 
   pl.xr = make_rsrc(static_cast<const uint8_t *>(x) + (size_t)m0 * K * xb, rows * K * xb);
   pl.x_voff = H ? r * K * 2 + h * 64 : (lane >> 4) * K * 4 + (lane & 15) * 16;
 
-  uint8_t *xt = smem + wave * XR * 128;
+  constexpr bool kStage = kStageWindow<P, KW, H>;
+  uint8_t *xt = smem + wave * XR * 128 * (kStage ? WIN : 1);
   Chunk<P, XR, H> win[WIN];
-#pragma unroll
-  for (int i = 0; i < WIN; ++i)
-    if (c0 + i < c1) load_chunk<P, XR, H>(win[i], pl, c0 + i);
   f32x16 acc[P];
 #pragma unroll
   for (int t = 0; t < P; ++t) acc[t] = (f32x16){};
+  uint32_t cfirst = c0;
+  if constexpr (kStage) {
+    // The first window at once: every slot's activations are loaded before
+    // any weight, staged into the slot's own tile and read back as fragments
+    // while the weights are still in flight, so the LDS round trip is off
+    // the path from the weights' arrival to the MFMAs.  Slots past the range
+    // load through zero-length resources (no memory access, zeros), which
+    // keeps every load unconditional and the waits exact.
+    const rsrc_t z = make_rsrc(qs, 0);
+#pragma unroll
+    for (int i = 0; i < WIN; ++i) load_acts(win[i], pl, c0 + i < c1 ? pl.xr : z, c0 + i);
+#pragma unroll
+    for (int i = 0; i < WIN; ++i)
+      load_weights(win[i], pl, c0 + i < c1 ? pl.wq : z, c0 + i < c1 ? pl.ws : z, c0 + i);
+    f16x8 xf[WIN][4];
+#pragma unroll
+    for (int i = 0; i < WIN; ++i) {
+      stage_acts(win[i], xt + i * XR * 128, lane);
+      read_frags<XR>(xt + i * XR * 128, lane, xf[i]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // zero slots add exactly nothing (their weights and scales are zeros)
+#pragma unroll
+    for (int i = 0; i < WIN; ++i) {
+      mfma_chunk(win[i], xf[i], acc);
+      if (c0 + i + WIN < c1) load_chunk<P, XR, H>(win[i], pl, c0 + i + WIN);
+    }
+    cfirst = c0 + WIN;
+  } else {
+#pragma unroll
+    for (int i = 0; i < WIN; ++i)
+      if (c0 + i < c1) load_chunk<P, XR, H>(win[i], pl, c0 + i);
+  }
 #pragma unroll 1
-  for (uint32_t c = c0; c < c1; c += WIN) {
+  for (uint32_t c = cfirst; c < c1; c += WIN) {
 #pragma unroll
     for (int i = 0; i < WIN; ++i) {
       if (c + i < c1) {
