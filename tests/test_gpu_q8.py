@@ -716,6 +716,9 @@ def staged_ok(c, x, qs, sc):
     # the batched decode step at M = 16: vocab (one panel per workgroup, tail panel),
     # q|k|v, FFN up and the 1280 x 1280 projections (single panels, unsplit)
     (16, 51866, 1280), (16, 3840, 1280), (16, 5120, 1280), (16, 1280, 1280),
+    # single panels, K unsplit (128 or more panels) and longer than one window
+    # per wave: the staged first window, then the chunk-by-chunk loop
+    (8, 5120, 4096), (3, 4096, 2048),
 ])
 def test_pproj_parity(q, m, n, k):
     say(f"pproj m={m} n={n} k={k}")
