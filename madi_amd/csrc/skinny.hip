@@ -395,13 +395,14 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 
 // waves split K, three chunks in flight each, so a K = 1280 range (2 - 3
 // chunks per wave) is one round of loads.  (Sixteen waves with two chunks
 // each measured slower: a workgroup's waves start up to ~0.8 us apart and the
-// reduction waits for the last.)  The vocab logits (1621 panels) up to 16
+// reduction waits for the last.)  The vocab logits (1621 panels) up to 8
 // rows: one panel per workgroup and four waves splitting K, two chunks in
-// flight each; 1621 workgroups spread evenly over the CUs, where 406 groups
-// of four panels leave a second, partial round (M = 8: 12.6 against 14.6 us,
-// M = 16: 14.2 against 15.5).  With 32-row slices the activations of a chunk
-// are four times the weight bytes, and four panels per workgroup sharing each
-// activation load stay ahead (M = 32: 17.2 against 19.5 us).
+// flight each; 1621 workgroups spread evenly over the CUs (M = 8: 14.05 us
+// against 14.92 with two panels per workgroup, cold weights).  From 9 rows
+// the activations of a chunk are twice the weight bytes or more, and every
+// panel's workgroup reads the whole slice, so four panels per workgroup share
+// each activation load (406 workgroups, two per CU: M = 16 16.24 against
+// 17.33 us with one panel, M = 32 17.2 against 19.5).
 constexpr int kPanelWaves = 8, kPanelWin = 3;
 constexpr int kVocabWaves = 4, kVocabWin = 2;
 constexpr int kGroupWaves = 4, kGroupWin = 2;
@@ -441,14 +442,14 @@ int launch_skinny(const Proj &a) {
   return check_launch(a.what);
 }
 
-// wide matrices (the vocab logits): one panel per workgroup up to 16 rows,
-// four panels sharing each activation load for 32-row slices; narrow ones
-// keep one panel per workgroup with eight waves
+// wide matrices (the vocab logits): one panel per workgroup up to 8 rows,
+// four panels sharing each activation load for 16- and 32-row slices; narrow
+// ones keep one panel per workgroup with eight waves
 template <int XR, bool H = false>
 int launch_rows(const Proj &a) {
   const uint32_t np = (a.n + kPanelRows - 1) / kPanelRows;
   if (np >= 1024) {
-    if constexpr (XR <= 16) return launch_skinny<1, kVocabWaves, XR, kVocabWin, H>(a);
+    if constexpr (XR <= 8) return launch_skinny<1, kVocabWaves, XR, kVocabWin, H>(a);
     return launch_skinny<4, kGroupWaves, XR, kGroupWin, H>(a);
   }
   return launch_skinny<1, kPanelWaves, XR, kPanelWin, H>(a);
