@@ -707,13 +707,14 @@ def staged_ok(c, x, qs, sc):
     (1, 3840, 1280), (2, 3840, 1280), (8, 5120, 1280), (16, 1280, 5120),
     (8, 51866, 1280),    # batched vocab logits, tail panel of 26 rows
     (24, 51866, 1280),   # vocab with 32-row slices: four panels per workgroup
-    (3, 51866, 1280), (13, 51866, 1280),  # vocab, 8- and 16-row tiles: rows past M
+    (3, 51866, 1280), (13, 51866, 1280),  # vocab, 8-row tiles (one panel per
+                                          # workgroup) and 16-row tiles (four): rows past M
     (32, 1280, 1280), (33, 3840, 1280), (70, 1280, 5120), (5, 40, 64),
     (17, 5120, 1280),    # one 32-row slice, 15 rows past M
     (320, 640, 1280),    # ten slices (M = 320, the prefill's largest) of 20 panels
     (192, 1280, 1280),   # six slices of 40 panels: 240 workgroups, the most that
                          # stay on the skinny kernel for a 1280 x 1280 weight
-    # the batched decode step at M = 16: vocab (one panel per workgroup, tail panel),
+    # the batched decode step at M = 16: vocab (four panels per workgroup, tail panel),
     # q|k|v, FFN up and the 1280 x 1280 projections (single panels, unsplit)
     (16, 51866, 1280), (16, 3840, 1280), (16, 5120, 1280), (16, 1280, 1280),
     # single panels, K unsplit (128 or more panels) and longer than one window
