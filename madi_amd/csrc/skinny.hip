@@ -406,6 +406,10 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 
 constexpr int kPanelWaves = 8, kPanelWin = 3;
 constexpr int kVocabWaves = 4, kVocabWin = 2;
 constexpr int kGroupWaves = 4, kGroupWin = 2;
+// Panel pairs (many 32-row slices of a narrow, short weight, where a
+// workgroup per panel and slice no longer fits one per CU): two panels share
+// each activation load, four waves split K.
+constexpr int kPairWaves = 4, kPairWin = 2;
 constexpr uint32_t kMaxSplits = 4;
 
 // One projection: out[m][n] = sum_k x[m][k] w[n][k]; x and out f32, or f16
@@ -484,14 +488,22 @@ extern "C" int madi_q8_pproj(float *out, const float *in, const void *qs, const 
   // per 32 or 64 rows of a tile that spans 128 or 256 outputs, where this
   // kernel dequantises it once per 32-row slice of a single panel.  Its tiles
   // take 7.5-11 us however few rows they hold (one K loop), so it pays from
-  // 160 rows on wide or long weights, and on narrower ones once this kernel's
-  // grid (a workgroup per panel and slice) no longer fits one per CU: 1280 x
-  // 1280 at M = 192 (240 workgroups) 5.1 us here against 7.7 on the GEMM,
-  // at M = 224 (280) 8.3 against 7.7 (measured, cold weights; M = 320:
-  // 1280->5120 12.3 vs 27.2 us, 1280->3840 12.2 vs 20.3, 5120->1280 19.0 vs
-  // 34.1).
-  const uint64_t skinny_wgs = (uint64_t)((n + kPanelRows - 1) / kPanelRows) * ((m + kSlice - 1) / kSlice);
-  if (m >= kGemmRows && (n >= 2048 || k >= 4096 || skinny_wgs > (uint64_t)cu_count()) &&
+  // 160 rows on wide or long weights (M = 320: 1280->5120 12.3 vs 27.2 us,
+  // 1280->3840 12.2 vs 20.3, 5120->1280 19.0 vs 34.1; measured, cold
+  // weights).  On narrower, shorter ones this kernel keeps a workgroup per
+  // panel and slice while that grid fits one per CU (1280 x 1280 at M = 160
+  // 4.8 us against 5.5 with panel pairs), then a workgroup per panel pair
+  // while that fits (M = 224 / 288 / 320: 5.6 / 5.8 / 5.9 us against 8.0 on
+  // the GEMM's 32 x 128 tiles, which leave 156 CUs idle), and only then the
+  // GEMM.
+  const uint64_t np = (n + kPanelRows - 1) / kPanelRows, slices = (m + kSlice - 1) / kSlice;
+  const uint64_t skinny_wgs = np * slices, cus = (uint64_t)cu_count();
+  if (m > kSlice && n < 2048 && k < 4096 && skinny_wgs > cus && (np + 1) / 2 * slices <= cus) {
+    const Proj a{out, in, static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), m, n,
+                 k, "madi_q8_pproj"};
+    return launch_skinny<2, kPairWaves, kSlice, kPairWin>(a);
+  }
+  if (m >= kGemmRows && (n >= 2048 || k >= 4096 || skinny_wgs > cus) &&
       n % kPanelRows == 0 && aligned(in, 16) &&
       aligned(out, 16) &&
       (uint64_t)m * k * 4 < (1ull << 31) && (uint64_t)n * 256 < (1ull << 31))

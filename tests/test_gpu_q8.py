@@ -720,6 +720,11 @@ def staged_ok(c, x, qs, sc):
     # single panels, K unsplit (128 or more panels) and longer than one window
     # per wave: the staged first window, then the chunk-by-chunk loop
     (8, 5120, 4096), (3, 4096, 2048),
+    # panel pairs (a workgroup per panel and slice would not fit the CUs):
+    # the prefill's 1280 x 1280 at M = 320 and 224, an odd panel count (the
+    # last pair holds one valid panel and a clamped one), and a partial last
+    # panel with an M tail and a 10-chunk K
+    (320, 1280, 1280), (224, 1280, 1280), (320, 1312, 1280), (300, 1000, 640),
 ])
 def test_pproj_parity(q, m, n, k):
     say(f"pproj m={m} n={n} k={k}")
@@ -738,11 +743,13 @@ def test_pproj_parity(q, m, n, k):
 # projection runs as the MFMA GEMM with f32 activations and an f32 result
 # (q8_gemm_kernel<MT, NONE, PADDED, true, false, PW>): 32 x 128, 64 x 128 and
 # 64 x 256 tiles, an M tail, a padded K loop (5 chunks over 4096 outputs) and
-# the 5120-wide K split over workgroups; 1280 x 1280 from 224 rows.
+# the 5120-wide K split over workgroups; 2048-wide weights at 224 and 288
+# rows (32 x 128 tiles), and 1280 x 1280 at 600 rows, where even panel pairs
+# would not fit the CUs.
 @pytest.mark.parametrize("m,n,k", [
     (160, 5120, 1280), (320, 3840, 1280), (320, 5120, 1280), (161, 4096, 320),
-    (320, 1280, 5120), (700, 2560, 1280), (256, 1280, 1280), (224, 1280, 1280),
-    (320, 1280, 1280),
+    (320, 1280, 5120), (700, 2560, 1280), (224, 2048, 1280), (288, 2048, 1280),
+    (600, 1280, 1280),
 ])
 def test_pproj_many_rows_gemm(q, m, n, k):
     say(f"pproj (GEMM) m={m} n={n} k={k}")
@@ -762,16 +769,16 @@ def test_pproj_many_rows_gemm(q, m, n, k):
 # in the same order and the same splits summed in the same order, so the f32
 # results equal the 256-column tiles' (MADI_GEMM_NARROW=0) bit for bit.
 # Shapes: the prefill's q|k|v, FFN up and FFN down (four splits) at M = 320
-# (64 x 128), its 1280 x 1280 projections and cross K|V (32 x 128), FFN up at
-# M = 160 (32 x 128), an M tail of 33 rows, 65 panels (the last tile holds one
-# valid panel and three clamped ones), FFN down at M = 160 (a 32-row tail
-# in a 64-row tile), 1280 x 1280 at M = 231 (a 7-row tail in a 32-row
-# tile), and a 96-wide weight with K = 4096 (one tile of three panels and a
-# clamped fourth, K split four ways).
+# (64 x 128), cross K|V (32 x 128), 1280 x 1280 at M = 600 (32 x 128), FFN
+# up at M = 160 (32 x 128), an M tail of 33 rows, 65 panels (the last tile
+# holds one valid panel and three clamped ones), FFN down at M = 160 (a
+# 32-row tail in a 64-row tile), a 2048-wide weight at M = 231 (a 7-row tail
+# in a 32-row tile), and a 96-wide weight with K = 4096 (one tile of three
+# panels and a clamped fourth, K split four ways).
 @pytest.mark.parametrize("m,n,k", [
     (320, 3840, 1280), (320, 5120, 1280), (161, 2048, 512), (320, 2080, 1280),
-    (320, 1280, 5120), (160, 1280, 5120), (320, 1280, 1280), (320, 2560, 1280),
-    (160, 5120, 1280), (231, 1280, 1280), (300, 96, 4096),
+    (320, 1280, 5120), (160, 1280, 5120), (600, 1280, 1280), (320, 2560, 1280),
+    (160, 5120, 1280), (231, 2048, 1280), (300, 96, 4096),
 ])
 def test_pproj_narrow_tiles_match_wide(q, m, n, k):
     import os
