@@ -491,8 +491,13 @@ def test_gemm_large_m(q):
 # (5120, 1280), (40, 64) one or two chunks per wave, (1280, 5120) four K
 # splits, (5120, 4096) four chunks per wave through the two-chunk window,
 # (40, 12288) the largest K in four splits of 48 chunks
+# Shapes: the vocab and the decoder projections; 40 panels at K = 64 (one
+# chunk: fifteen of the sixteen waves own none); 5120 x 4096 (four chunks per
+# wave, past the first window); 40 x 12288 (K split over workgroups); and
+# wide matrices (256 or more panels, four waves, the fp32 vector read one
+# unit ahead) at K = 64 and 192, where some waves own no chunk and others one.
 @pytest.mark.parametrize("n,k", [(51866, 1280), (3840, 1280), (1280, 5120), (5120, 1280), (40, 64),
-                                 (5120, 4096), (40, 12288)])
+                                 (5120, 4096), (40, 12288), (8200, 64), (8192, 192)])
 def test_gemv_parity(q, n, k):
     say(f"gemv n={n} k={k}")
     x16, qs, sc = synth.gemv_case(n + k, n, k)
