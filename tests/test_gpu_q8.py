@@ -821,6 +821,23 @@ def test_pproj_many_rows_one_hot(q):
     assert np.array_equal(c, ref)
 
 
+@pytest.mark.parametrize("n", [1280, 1312])
+def test_pproj_panel_pairs_one_hot(q, n):
+    """One-hot rows through the panel-pair route (256 rows of a 1280-long
+    weight: a workgroup per panel and slice would not fit the CUs, a
+    workgroup per pair does; 1312 = 41 panels leaves the last pair one valid
+    panel): the f32 results equal the dequantised weights bit for bit."""
+    k = 1280
+    rng = np.random.default_rng(23)
+    qs, sc = synth.q8_weight(rng, n, k)
+    ks = (np.arange(256) * 37) % k
+    x = np.zeros((len(ks), k), np.float32)
+    x[np.arange(len(ks)), ks] = 1.0
+    c = _pproj(q, x, qs, sc)
+    ref = O.dequant_q8_f16(qs, sc)[ks].astype(np.float32)
+    assert np.array_equal(c, ref)
+
+
 def test_pproj_one_hot_is_dequant(q):
     """x = one-hot rows: out[m][n] = fp16_rne(q s) of column k_m, bit-exact."""
     n, k = 96, 128
