@@ -838,6 +838,22 @@ def test_pproj_panel_pairs_one_hot(q, n):
     assert np.array_equal(c, ref)
 
 
+@pytest.mark.parametrize("m", [8, 16])
+def test_pproj_vocab_one_hot(q, m):
+    """One-hot rows through the vocab's launch shapes (8 rows: one panel per
+    workgroup; 16: four panels per workgroup, the last group ending in the
+    26-row tail panel): the f32 results equal the dequantised weights."""
+    n, k = 51866, 1280
+    rng = np.random.default_rng(29 + m)
+    qs, sc = synth.q8_weight(rng, n, k)
+    ks = np.array([0, 31, 32, 63, 64, 640, 1247, 1279, 5, 97, 300, 511, 512, 700, 1000, 1200])[:m]
+    x = np.zeros((m, k), np.float32)
+    x[np.arange(m), ks] = 1.0
+    c = _pproj(q, x, qs, sc)
+    ref = O.dequant_q8_f16(qs, sc)[ks].astype(np.float32)
+    assert np.array_equal(c, ref)
+
+
 def test_pproj_one_hot_is_dequant(q):
     """x = one-hot rows: out[m][n] = fp16_rne(q s) of column k_m, bit-exact."""
     n, k = 96, 128
