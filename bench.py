@@ -2,14 +2,17 @@
 
 A step is one pass of the hot path over one batch of synthetic input:
   1. the encoder fc1 Q8 GEMM, A f16 [1500, 1280] x W int8 [5120, 1280] (+ fp16
-     per-32 scales) -> C f16 [1500, 5120], fp32 accumulation, and
+     per-32 scales) -> C f16 [1500, 5120], fp32 accumulation;
   2. the decoder vocab-logit Q8 GEMV, x f16 [1280] x W int8 [51866, 1280] ->
      f32 logits [51866], cold: the step cycles through 4 distinct weight copies
-     (4 x 70.75 MB > the 256 MB Infinity Cache) so each launch streams HBM.
+     (4 x 70.75 MB > the 256 MB Infinity Cache) so each launch streams HBM;
+  3. the same vocab GEMV with f32 activations, as the engine calls it
+     (kLogitGemv, madi_q8_logit_gemv), on the same rotation.
 Inputs are resident in HBM before the timed region.  The timed region runs
-the K steps' GEMMs back to back and then their GEMVs, with HIP events on the
-kernels' stream at the start, between the two runs and at the end, so each
-kernel's average duration is (event span) / K -- the figure rocprofv3's
+the K steps' GEMMs back to back, then their fp16-activation GEMVs, then their
+f32-activation GEMVs, with HIP events on the kernels' stream at the start,
+between the runs and at the end, so each kernel's average duration is
+(event span) / K -- the figure rocprofv3's
 kernel trace reports for the same launches (a per-launch event pair would add
 the dispatch gap).  The JSON line reports the GEMM as the headline value
 (TFLOP/s) and the GEMV beside it (GB/s), each with its roofline fraction and,
@@ -146,16 +149,21 @@ DEC_SHAPES = [("self_qkv", 3840, 1280), ("self_out", 1280, 1280), ("cross_q", 12
               ("cross_out", 1280, 1280), ("ffn_up", 5120, 1280), ("ffn_down", 1280, 5120)]
 
 
-def _timed(torch, stream, fn, reps):
+def _timed(torch, stream, fn, reps, settle=False):
     """Average seconds per call of fn() over `reps` back-to-back calls, after
     untimed calls with the last min(reps, 8) indices (the first shape of a
     configuration otherwise pays for the clocks ramping up after the set-up's
     copies; the timed calls then start with the weight copy used longest ago,
-    as in the steady state of the rotation)."""
+    as in the steady state of the rotation).  The timed calls follow the
+    untimed ones with the GPU still busy, the steady state of the engine's
+    loops; with `settle` the host waits for the GPU in between, so the timed
+    region starts from an idle GPU and shows the rate at which the caller
+    issues (the Python-issued figures)."""
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for i in range(max(reps - 8, 0), reps):
         fn(i)
-    torch.cuda.synchronize()
+    if settle:
+        torch.cuda.synchronize()
     e0.record(stream)
     for i in range(reps):
         fn(i)
@@ -166,10 +174,10 @@ def _timed(torch, stream, fn, reps):
 
 def _timed_list(torch, stream, lst, reps, per=1):
     """Average seconds per `per` calls' worth of lst (an IssueList replayed from
-    C) over `reps` back-to-back replays, after min(reps, 4) untimed ones."""
+    C) over `reps` back-to-back replays, after min(reps, 4) untimed ones that
+    are still running when the timed replays start."""
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     lst.run(min(reps, 4))
-    torch.cuda.synchronize()
     e0.record(stream)
     lst.run(reps)
     e1.record(stream)
@@ -328,7 +336,7 @@ def config_batched_decode(torch, stream, q8, reps=20):
             q.pproj(xin, vocab, out, m, VOCAB, DIM)
         step(0)
         step(1)
-        tp = _timed(torch, stream, step, reps)
+        tp = _timed(torch, stream, step, reps, settle=True)
         two = IssueList()   # two steps, one per weight set
         step(0, lst=two)
         step(1, lst=two)
@@ -404,7 +412,7 @@ def config_decode_token(torch, stream, q8, reps=20):
     from madi_amd.issue import IssueList
     token(0)
     token(1)
-    tp = _timed(torch, stream, token, reps)
+    tp = _timed(torch, stream, token, reps, settle=True)
     two = IssueList()   # two tokens, one per weight set
     token(0, two)
     token(1, two)
@@ -434,7 +442,10 @@ def config_decode_token(torch, stream, q8, reps=20):
         tq, ts = (t_.clone() for t_ in base._keep)
         ws.append(q8.Q8(tq.data_ptr(), ts.data_ptr(), (tq, ts)))
     q8.kQkv(q, xb, ws[0], qb, vb, kc, vc, pos, d)
-    tq = _timed(torch, stream, lambda i: q8.kQkv(q, xb, ws[i % 64], qb, vb, kc, vc, pos, d), 64)
+    rot = IssueList()   # the 64 copies in turn, issued from C (a ~4 us kernel)
+    for w in ws:
+        rot.kQkv(q, xb, w, qb, vb, kc, vc, pos, d)
+    tq = _timed_list(torch, stream, rot, 2, per=64)
     qb_bytes = 3 * d * d + 3 * d * (d // 32) * 2
     res["qkv_gemv"] = {"us": round(tq * 1e6, 2), "gbs": round(qb_bytes / tq / 1e9, 1),
                        "frac_hbm_peak": round(qb_bytes / tq / 1e9 / PEAK_HBM_GBS, 4)}
@@ -642,9 +653,13 @@ def main():
     for i in range(args.warmup):
         gemm(i)
         gemv(i)
+        logit(i)
     torch.cuda.synchronize()
 
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    # One step: the fc1 GEMM, the vocab GEMV with fp16 activations and the
+    # engine's f32-activation vocab GEMV.  The three loops run back to back in
+    # one synchronised region, each timed by events on the stream.
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
     log(f"timing {args.steps} steps")
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -655,13 +670,14 @@ def main():
     for i in range(args.steps):
         gemv(i)
     ev[2].record(stream)
+    for i in range(args.steps):
+        logit(i)
+    ev[3].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     g_avg = ev[0].elapsed_time(ev[1]) * 1e-3 / args.steps   # s per GEMM launch
     v_avg = ev[1].elapsed_time(ev[2]) * 1e-3 / args.steps   # s per GEMV launch
-    for i in range(args.warmup):
-        logit(i)
-    l_avg = _timed(torch, stream, logit, args.steps)           # s per f32-x GEMV launch
+    l_avg = ev[2].elapsed_time(ev[3]) * 1e-3 / args.steps   # s per f32-x GEMV launch
     l_gbs = (gemv_bytes() + DIM * 2) / l_avg / 1e9              # x is f32: 2 more bytes per element
     gemm_tflops = gemm_flops() / g_avg / 1e12
     gemv_gbs = gemv_bytes() / v_avg / 1e9
