@@ -10,7 +10,7 @@
 // row r in quantisation block h), issued as a buffer load with the
 // panel/chunk offset in an SGPR.  Each wave streams its K range through a
 // two-chunk window (use chunk c, refill with chunk c+2).  The four-wave
-// instances keep to 48 - 65 VGPRs (seven waves per SIMD), so every workgroup
+// instances keep to 62 - 71 VGPRs (seven waves per SIMD allow 72), so every workgroup
 // of the 51866-row vocab matrix (1621 panels, seven per CU) is resident from
 // the start; the sixteen-wave ones (four waves per SIMD) take up to 94.
 //
