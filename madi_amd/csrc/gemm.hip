@@ -23,12 +23,13 @@
 //            chunks ahead of use, into WD rotating register sets;
 //   A        the 32*MT x 64 f16 activation tile is shared by the four waves
 //            through an NA-stage LDS ring, written by direct-to-LDS DMA
-//            (buffer_load_dwordx4 ... lds) NA-1 chunks ahead; the 16-byte
+//            (buffer_load_dwordx4 ... lds) DA chunks ahead; the 16-byte
 //            chunks of row r are XOR-swizzled by (r >> 1) & 7 so each DMA
 //            instruction copies 8 whole 128-byte rows and the fragment reads
 //            (32 consecutive rows, one chunk each) spread over all banks.
-// One barrier per chunk (before its last k-step) publishes the next chunk's A
-// stage and retires the oldest one.
+// One barrier per two chunks (before the last k-step of each odd chunk c)
+// publishes the A stages of chunks c+1 and c+2 and retires those of c-1 and
+// c.
 //
 // Weight fragments: register w[t][s] holds panel t's k-step-s fragment.  It
 // is consumed by the MFMAs of step s and refilled in place with the next
