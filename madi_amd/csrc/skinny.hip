@@ -13,8 +13,9 @@
 // the result away from the fp32 reference of test_batchproj.zig:72-78).
 //
 // Workgroup: P weight panels (32 rows each; P = 4 for the 51866-row vocab
-// matrix with 32-row slices, 1 otherwise) x one slice of 32 activation rows
-// (the MFMA columns), KW waves splitting K.  Per 64-wide K chunk a wave loads each panel's two
+// matrix from 9 rows, 2 for narrow weights at prefill sizes (panel pairs),
+// 1 otherwise) x one slice of 32 activation rows (the MFMA columns), KW
+// waves splitting K.  Per 64-wide K chunk a wave loads each panel's two
 // 16-byte units per lane (lane (h, r): row r's 32 weights of quantisation
 // block h) and scale, and the slice's first XR rows (8, 16 or 32: the rows a
 // batch of M <= XR has) of 64 f32 activations with coalesced loads (each
