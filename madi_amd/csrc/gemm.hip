@@ -63,7 +63,7 @@
 // (700 x 5120 -> 1280: 55 tiles of 64 x 256; the batched projection's FFN
 // down at M = 320: 50 tiles of 64 x 128), up to four workgroups share a tile,
 // each over a contiguous K range.  Each publishes its fp32 partial tile to
-// the library's workspace and counts itself in with a system-scope atomic;
+// the library's workspace and counts itself in with a device-scope atomic;
 // the last to arrive adds the partials in split order and runs the epilogue.
 // The grid is one-dimensional over (tile, split) items, renumbered so that
 // each XCD runs a contiguous share of them (the tile order, below).
@@ -949,8 +949,9 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     // counts itself in; the last to arrive adds the others' partials to its
     // own and finishes the tile.  The partials are written and read with
     // device-scope (sc1) buffer accesses, which write through and read past
-    // the XCD's own L2, and the count is a system-scope atomic, so no L2-wide
-    // writeback or invalidate is needed.
+    // the XCD's own L2, and the count is a device-scope atomic (every party is
+    // a workgroup of this launch), so no L2-wide writeback or invalidate is
+    // needed.
     constexpr uint32_t kPart = 4 * PW * MT * 4 * 64 * 16;  // bytes per partial tile
     const __amdgpu_buffer_rsrc_t wsr =
         __builtin_amdgcn_make_buffer_rsrc(ws, 0, (int)(T * splits * kPart), 0x00020000);
@@ -968,7 +969,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the partial has been written through
     __syncthreads();
     if (threadIdx.x == 0)
-      arrived = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      arrived = __hip_atomic_fetch_add(&cnt[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (arrived != splits - 1) return;
     constexpr int kGroups = PW * MT * 4;  // register groups q = (t, i, g) in order
@@ -1043,7 +1044,7 @@ __global__ __launch_bounds__(256) void q8_gemm_kernel(
     }
     }
     if (threadIdx.x == 0)  // ready for the next launch
-      __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      __hip_atomic_store(&cnt[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   }
   const OutTile ot = out_tile(seg, Cout, bias, N, p0);

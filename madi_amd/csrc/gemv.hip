@@ -361,26 +361,27 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(kWavesP
     for (int w = 1; w < KW; ++w) v += red[w * 32 + t];
   }
   if (a.splits > 1) {
-    // Split K: each workgroup writes its 32 partial row sums through to memory
-    // (system-scope stores) and counts itself in; the last to arrive adds the
+    // Split K: each workgroup writes its 32 partial row sums past its XCD's L2
+    // (device-scope stores) and counts itself in with a device-scope atomic
+    // (every party is a workgroup of this launch); the last to arrive adds the
     // splits' partials in split order (the same order whoever arrives last)
     // and stores the rows.
     __shared__ uint32_t arrived;
     float *mine = a.ws + ((size_t)p * a.splits + split) * 32;
-    if (t < 32) __hip_atomic_store(mine + t, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (t < 32) __hip_atomic_store(mine + t, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (t == 0)
-      arrived = __hip_atomic_fetch_add(&a.cnt[p], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+      arrived = __hip_atomic_fetch_add(&a.cnt[p], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (arrived != a.splits - 1) return;
     if (t < 32) {
       const float *all = a.ws + (size_t)p * a.splits * 32 + t;
       v = 0.0f;
       for (uint32_t s2 = 0; s2 < a.splits; ++s2)
-        v += __hip_atomic_load(all + s2 * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        v += __hip_atomic_load(all + s2 * 32, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    if (t == 0) __hip_atomic_store(&a.cnt[p], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (t == 0) __hip_atomic_store(&a.cnt[p], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   if (t >= R) return;
   const uint32_t nrow = erow;  // t == threadIdx.x
