@@ -92,7 +92,12 @@ int madi_begin_command_buffer(void);
 int madi_commit_command_buffer(void);
 int madi_sync(void);
 /* No reference counterpart: lets a host that owns a HIP stream (hipStream_t
- * passed as void*) order this library's launches on it.  NULL = null stream. */
+ * passed as void*) order this library's launches on it.  NULL = null stream.
+ * The new stream first waits (on the device, the host does not block) for
+ * the work already issued on the old one, so the library's launches stay in
+ * call order across the switch.  Where either stream is under graph capture
+ * no such wait is added (a capture may not wait on outside work): the caller
+ * orders the two streams, e.g. synchronises before capturing. */
 int madi_set_stream(void *hip_stream);
 /* Message of the last failure on the calling thread ("" if none). */
 const char *madi_last_error(void);

@@ -18,6 +18,8 @@ thread_local char g_err[512] = "";
 bool g_init = false;
 int g_cu_count = 0;
 hipStream_t g_stream = nullptr;
+// Orders a newly chosen stream after the work already issued on the old one.
+hipEvent_t g_switch = nullptr;
 // Split-K workspace: kCounters zeroed arrival counters, then the partial sums.
 constexpr size_t kCounters = 16384;
 void *g_ws = nullptr;
@@ -144,6 +146,14 @@ extern "C" int madi_init(void) {
     g_init = false;
     return rc;
   }
+  if (!g_switch) {
+    e = hipEventCreateWithFlags(&g_switch, hipEventDisableTiming);
+    if (e != hipSuccess) {
+      g_switch = nullptr;
+      g_init = false;
+      return fail(MADI_ERR_INIT, "madi_init: hipEventCreate: %s", hipGetErrorString(e));
+    }
+  }
   g_err[0] = 0;
   return MADI_OK;
 }
@@ -154,6 +164,8 @@ extern "C" void madi_cleanup(void) {
   (void)hipStreamSynchronize(g_stream);
   free_workspace();
   f16gemm_cleanup();
+  if (g_switch) (void)hipEventDestroy(g_switch);
+  g_switch = nullptr;
   g_stream = nullptr;
   g_init = false;
 }
@@ -225,10 +237,30 @@ extern "C" int madi_sync(void) {
 }
 
 extern "C" int madi_set_stream(void *s) {
-  // work held for a later launch goes to the stream it was issued on
-  if (g_init)
+  const hipStream_t ns = reinterpret_cast<hipStream_t>(s);
+  if (g_init) {
+    // work held for a later launch goes to the stream it was issued on
     if (int rc = group_flush()) return rc;
-  g_stream = reinterpret_cast<hipStream_t>(s);
+    // The library's launches stay in call order across the switch: the new
+    // stream waits for what the old one holds (split-K launches on the two
+    // would otherwise share the workspace's partials and counters at once).
+    // A stream under graph capture may not wait on work outside it, so
+    // around a capture the caller orders the two streams itself.  The new
+    // stream is asked first: entering a capture, the old one (often the
+    // legacy null stream, which must not be queried while another stream
+    // captures) is left alone.
+    hipStreamCaptureStatus a = hipStreamCaptureStatusNone, b = hipStreamCaptureStatusNone;
+    if (ns != g_stream && hipStreamIsCapturing(ns, &b) == hipSuccess &&
+        b == hipStreamCaptureStatusNone && hipStreamIsCapturing(g_stream, &a) == hipSuccess &&
+        a == hipStreamCaptureStatusNone) {
+      hipError_t e = hipEventRecord(g_switch, g_stream);
+      if (e == hipSuccess) e = hipStreamWaitEvent(ns, g_switch, 0);
+      if (e != hipSuccess)
+        return fail(MADI_ERR_DISPATCH, "madi_set_stream: ordering the new stream: %s",
+                    hipGetErrorString(e));
+    }
+  }
+  g_stream = ns;
   return MADI_OK;
 }
 

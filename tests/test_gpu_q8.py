@@ -1076,3 +1076,49 @@ def test_f16_gemm_kM4_epilogues(q, epi):
             v = np.vectorize(O.gelu_erf, otypes=[np.float32])(v)
         ref = O.f32_to_f16(v).astype(np.float64)
     assert normwise(got, ref) <= TOL
+
+
+def test_stream_switch_orders_split_k(q):
+    """madi_set_stream makes the new stream wait for the work already issued
+    on the old one.  Split-K launches (the FFN-down GEMV 5120 -> 1280, four K
+    splits, and the GEMM 1000 x 5120 -> 1280, three K splits through the
+    workspace) go to two streams in turn while the first is still busy with
+    twenty such GEMMs.  They share the workspace's partials and arrival
+    counters one after the other, so every output equals its single-stream
+    result bit for bit, round after round (counters left off zero would show
+    in the later rounds)."""
+    say("stream switch: split-K launches on two streams")
+    rng = np.random.default_rng(41)
+    qs1, sc1 = synth.q8_weight(rng, 1280, 5120)
+    w1 = q.upload_q8(qs1, sc1)
+    xs = [dev(rng.standard_normal(5120).astype(np.float32)) for _ in range(4)]
+    a = dev_f16(synth.activations(rng, 1000, 5120))
+    c = torch.empty((1000, 1280), dtype=torch.int16, device="cuda")
+    outs = [torch.empty(1280, dtype=torch.float32, device="cuda") for _ in range(4)]
+    q.init()
+    for x, o in zip(xs, outs):
+        q.kGemvQ8(o, x, w1, 1280, 5120)
+    q.kGemmQ8(a, w1, c, 1000, 1280, 5120)
+    q.sync()
+    want, want_c = [o.clone() for o in outs], c.clone()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+    for rep in range(3):
+        for o in outs:
+            o.fill_(float("nan"))
+        c.fill_(0)
+        torch.cuda.synchronize()
+        q.init(s1)
+        for _ in range(20):
+            q.kGemmQ8(a, w1, c, 1000, 1280, 5120)
+        q.kGemvQ8(outs[0], xs[0], w1, 1280, 5120)
+        q.kGemvQ8(outs[1], xs[1], w1, 1280, 5120)
+        q.init(s2)
+        q.kGemvQ8(outs[2], xs[2], w1, 1280, 5120)
+        q.kGemmQ8(a, w1, c, 1000, 1280, 5120)
+        q.init(s1)
+        q.kGemvQ8(outs[3], xs[3], w1, 1280, 5120)
+        torch.cuda.synchronize()
+        for i, (o, w) in enumerate(zip(outs, want)):
+            assert torch.equal(o, w), (rep, i)
+        assert torch.equal(c, want_c), rep
+    q.init()
