@@ -54,8 +54,30 @@ def host_f16(t):
     return t.cpu().numpy().view(np.float16)
 
 
+# The F16 scratch buffers the tests hand to kDeq / deqW16 (torch memory).
+_SENTINELS = []
+
+
 def sentinel(n):
-    return torch.from_numpy(np.full(n, NAN16, np.uint16).view(np.int16)).cuda()
+    t = torch.from_numpy(np.full(n, NAN16, np.uint16).view(np.int16)).cuda()
+    _SENTINELS.append(t)
+    return t
+
+
+@pytest.fixture(autouse=True)
+def _retire_records():
+    """After each test, drop the deferred-dequantisation records on its F16
+    scratch buffers (madi_q8_forget over each whole buffer: the records are
+    dropped, nothing is written), as a host does before its allocator hands
+    the memory to other code.  A record left on freed torch memory would be
+    written out into whatever a later test allocates there once that test's
+    writes overlap it."""
+    yield
+    if _SENTINELS:
+        import madi_amd.q8 as q8
+        for t in _SENTINELS:
+            q8.forget(t)
+        _SENTINELS.clear()
 
 
 def normwise(c, ref):
