@@ -222,33 +222,77 @@ extern "C" uint64_t madi_q8_fnv(uint64_t seed, const void *qs, size_t nq, const 
 }
 
 // ------------------------------------------------------------------ dequant -> F16 [K][N]
-// grid (ceil(R*K/16 / 256), panels): one thread per panel-layout 16-byte unit.
-// Consecutive lanes hold consecutive rows r, so each of the 16 stores writes
-// 32 consecutive n of one output row k (coalesced 64-byte runs).  Only the
-// elements with index in [lo, hi) are written (the whole matrix, [0, n*k),
-// for kDeq; a window when part of the destination has since been overwritten).
+// grid (ceil(panels / 4), K / 64): a workgroup dequantises four panels (128
+// columns n of the output) for one 64-wide chunk of K into an LDS tile, then
+// writes the tile out row by row.  Loading, lane (panel, j, h, row pair)
+// takes the panel-layout units of rows r and r+1 (32 contiguous bytes) and
+// writes each k's two values as one 4-byte LDS word.  Storing, each output
+// row k of the tile is 256 contiguous bytes: 16-byte stores (16 lanes per
+// row) where N % 8 == 0 and the output is 16-byte aligned (every encoder
+// shape), else 2-byte stores with n fastest (128 contiguous bytes per wave
+// instruction; the 51866-row vocab).  Only the elements with index in
+// [lo, hi) are written (the whole matrix, [0, n*k), for kDeq; a window when
+// part of the destination has since been overwritten).
+constexpr uint32_t kDeqPanels = 4;
+// LDS row pitch: 128 f16 plus 16 bytes, so consecutive rows start in
+// different banks and every 16-byte piece stays aligned
+constexpr uint32_t kDeqPitch = kDeqPanels * kPanelRows * 2 + 16;
+
 __global__ __launch_bounds__(256) void q8_dequant_f16_kernel(f16 *__restrict__ out,
                                                              const uint8_t *__restrict__ qs,
                                                              const f16 *__restrict__ sc,
                                                              uint32_t n, uint32_t k, size_t lo,
-                                                             size_t hi) {
-  const uint32_t p = blockIdx.y, R = panel_rows(n, p);
-  const uint32_t u = blockIdx.x * 256 + threadIdx.x;
-  if (u >= R * (k / 16)) return;
-  const uint32_t per_chunk = 4 * R;  // units per chunk
-  const uint32_t c = u / per_chunk, rem = u % per_chunk;
-  const uint32_t jh = rem / R, r = rem % R, j = jh / 2, h = jh % 2;
-  const u32x4 w = *reinterpret_cast<const u32x4 *>(qs + panel_chunk_qs(k, p, R, c) + rem * 16);
-  const f16 s = sc[panel_chunk_sc(k, p, R, c) + h * R + r];
-  f16x8 lo8, hi8;
-  dequant16(w, s, lo8, hi8);
-  const uint32_t col = p * kPanelRows + r;
-  const uint32_t k0 = c * kChunkK + h * 32 + j * 16;
+                                                             size_t hi, uint32_t vec) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kChunkK * kDeqPitch];
+  const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
+  const uint32_t g = blockIdx.x, c = blockIdx.y, t = threadIdx.x;
+  {
+    // one wave per panel; 16 lanes per (j, h), each with rows 2rp, 2rp + 1
+    const uint32_t pl = t >> 6, jh = (t >> 4) & 3, rp = t & 15;
+    const uint32_t p = g * kDeqPanels + pl, r = 2 * rp;
+    if (p < np) {
+      const uint32_t R = panel_rows(n, p);
+      if (r < R) {
+        const uint32_t j = jh >> 1, h = jh & 1;
+        const uint8_t *u = qs + panel_chunk_qs(k, p, R, c) + ((2 * j + h) * R + r) * 16;
+        const f16 *s = sc + panel_chunk_sc(k, p, R, c) + h * R + r;
+        const bool two = r + 1 < R;
+        f16x8 a0, a1, b0 = {}, b1 = {};
+        dequant16(*reinterpret_cast<const u32x4 *>(u), s[0], a0, a1);
+        if (two) dequant16(*reinterpret_cast<const u32x4 *>(u + 16), s[1], b0, b1);
+        const uint32_t k0 = h * 32 + j * 16, col = pl * kPanelRows + r;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const size_t e0 = (size_t)(k0 + i) * n + col, e1 = (size_t)(k0 + 8 + i) * n + col;
-    if (e0 >= lo && e0 < hi) out[e0] = lo8[i];
-    if (e1 >= lo && e1 < hi) out[e1] = hi8[i];
+        for (int i = 0; i < 8; ++i) {
+          *reinterpret_cast<f16x2 *>(tile + (k0 + i) * kDeqPitch + col * 2) = (f16x2){a0[i], b0[i]};
+          *reinterpret_cast<f16x2 *>(tile + (k0 + 8 + i) * kDeqPitch + col * 2) = (f16x2){a1[i], b1[i]};
+        }
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t n0 = g * kDeqPanels * kPanelRows;
+  if (vec) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint32_t idx = t + 256 * s, kr = idx >> 4, c8 = idx & 15, nn = n0 + c8 * 8;
+      if (nn >= n) continue;  // N % 8 == 0: a group is wholly inside or outside
+      const size_t e = (size_t)(c * kChunkK + kr) * n + nn;
+      const f16x8 v = *reinterpret_cast<const f16x8 *>(tile + kr * kDeqPitch + c8 * 16);
+      if (e >= lo && e + 8 <= hi) {
+        *reinterpret_cast<f16x8 *>(out + e) = v;
+      } else if (e + 8 > lo && e < hi) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          if (e + i >= lo && e + i < hi) out[e + i] = v[i];
+      }
+    }
+  } else {
+    for (int s = 0; s < 32; ++s) {
+      const uint32_t idx = t + 256 * s, kr = idx >> 7, nl = idx & 127, nn = n0 + nl;
+      if (nn >= n) continue;
+      const size_t e = (size_t)(c * kChunkK + kr) * n + nn;
+      if (e >= lo && e < hi) out[e] = *reinterpret_cast<const f16 *>(tile + kr * kDeqPitch + nl * 2);
+    }
   }
 }
 
@@ -256,11 +300,12 @@ namespace madi {
 int dequant_launch(void *wdq, const void *qs, const void *scales, uint32_t n, uint32_t k,
                    size_t lo, size_t hi) {
   const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
-  const uint32_t units = kPanelRows * (k / 16);
   if (hi > (size_t)n * k) hi = (size_t)n * k;
-  hipLaunchKernelGGL(q8_dequant_f16_kernel, dim3((units + 255) / 256, np), dim3(256), 0,
-                     stream(), static_cast<f16 *>(wdq), static_cast<const uint8_t *>(qs),
-                     static_cast<const f16 *>(scales), n, k, lo, hi);
+  const uint32_t vec = n % 8 == 0 && aligned(wdq, 16) ? 1u : 0u;
+  hipLaunchKernelGGL(q8_dequant_f16_kernel, dim3((np + kDeqPanels - 1) / kDeqPanels, k / kChunkK),
+                     dim3(256), 0, stream(), static_cast<f16 *>(wdq),
+                     static_cast<const uint8_t *>(qs), static_cast<const f16 *>(scales), n, k, lo,
+                     hi, vec);
   return check_launch("madi_q8_dequant_f16");
 }
 }  // namespace madi
