@@ -2,8 +2,8 @@
  * q8_oracle.h -- CPU restatement of the reference's Q8 matmul arithmetic.
  *
  * TEST INFRASTRUCTURE ONLY.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the checker
- * (or, for bench.py, as the timed restated-reference CPU path).  The product
+ * cpu_baseline leg of bench.py may load this library, and only to check
+ * results (or, for bench.py, as the timed restated-reference CPU path).  The product
  * library (madi_amd) never links, loads or calls it.
  *
  * Every routine works on the reference's NATURAL Q8_0 layout:

@@ -2,7 +2,7 @@
 
 Every call goes through the C ABI (libmadi_q8.so via ctypes); torch only
 provides device buffers.  Bars: bit-exact for the dequantised weights and the
-layout work; normwise max|C - C_ref| / max|C_ref| <= 1e-3 (the north-star
+layout work; normwise max|C - C_ref| / max|C_ref| <= 1e-3 (the path's
 tolerance) for the GEMM/GEMV, where C_ref is the oracle's
 dequantise-then-fp32-accumulate result.
 """

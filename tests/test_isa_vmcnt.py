@@ -85,8 +85,8 @@ def test_every_attention_instance_is_race_free(attn_asm):
     assert not bad, bad
 
 
-def test_checker_catches_a_premature_read():
-    """The checker itself: a read of a load's destination before its wait,
+def test_wait_check_catches_a_premature_read():
+    """The wait check itself: a read of a load's destination before its wait,
     and a register reused while a dead load is in flight, are both flagged;
     the waited read is not."""
     asm = ["buffer_load_dwordx4 v[4:7], v1, s[0:3], s4 offen",
