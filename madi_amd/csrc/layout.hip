@@ -337,7 +337,7 @@ __device__ inline float panel_weight(const uint8_t *qs, const f16 *sc, uint32_t 
 
 // gpu_emb_lookup_q8 / emb_lookup_indirect_q8 semantics (graph_helpers.metal:354-383).
 // `n_rows` bounds the token: an out-of-range token writes nothing (the
-// reference reads out of bounds there; this build refuses instead).
+// reference reads out of bounds there; this library refuses instead).
 __global__ __launch_bounds__(256) void q8_emb_row_kernel(float *__restrict__ out,
                                                          const uint8_t *__restrict__ qs,
                                                          const f16 *__restrict__ sc,
