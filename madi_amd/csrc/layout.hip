@@ -86,32 +86,54 @@ extern "C" int madi_q8_unpack_host(void *dst_qs, void *dst_scales, const void *t
 
 // ------------------------------------------------------------------ device repack
 // One thread per natural 16-byte unit (reads coalesced along the row).
-__global__ __launch_bounds__(256) void q8_repack_qs_kernel(uint8_t *__restrict__ dst,
-                                                           const int8_t *__restrict__ src,
-                                                           uint32_t n, uint32_t k,
-                                                           size_t units) {
-  size_t u = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (u >= units) return;
-  const uint32_t upr = k / 16;
-  const uint32_t row = (uint32_t)(u / upr), kk = (uint32_t)(u % upr) * 16;
-  const uint32_t p = row / kPanelRows, r = row % kPanelRows, R = panel_rows(n, p);
-  const uint32_t c = kk / kChunkK, h = (kk % kChunkK) / 32, j = (kk % 32) / 16;
-  u32x4 w = *reinterpret_cast<const u32x4 *>(src + (size_t)row * k + kk);
-  w ^= (u32x4){0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};  // q + 128 per byte
-  *reinterpret_cast<u32x4 *>(dst + panel_chunk_qs(k, p, R, c) + ((2 * j + h) * R + r) * 16) = w;
-}
+// Natural rows -> panel layout on the device.  Grid (panels, ceil(K / 256)):
+// a workgroup moves one panel's rows over four 64-wide chunks.  The rows are
+// read whole (8 lanes per 256-byte row segment, 32 bytes each, flipped to
+// q + 128) into an LDS tile; the units then leave in the panel layout's own
+// order, so consecutive lanes write consecutive 16-byte units (the four
+// chunks of a full panel are 8 KiB contiguous).  The scales (8 per row) go
+// straight to their panel positions.
+constexpr uint32_t kRepackChunks = 4;
+constexpr uint32_t kRepackPitch = kRepackChunks * kChunkK + 16;  // LDS row bytes
 
-__global__ __launch_bounds__(256) void q8_repack_sc_kernel(uint16_t *__restrict__ dst,
-                                                           const uint16_t *__restrict__ src,
-                                                           uint32_t n, uint32_t k,
-                                                           size_t count) {
-  size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (e >= count) return;
-  const uint32_t nb = k / 32;
-  const uint32_t row = (uint32_t)(e / nb), b = (uint32_t)(e % nb);
-  const uint32_t p = row / kPanelRows, r = row % kPanelRows, R = panel_rows(n, p);
-  const uint32_t c = b / 2, h = b % 2;
-  dst[panel_chunk_sc(k, p, R, c) + h * R + r] = src[e];
+__global__ __launch_bounds__(256) void q8_repack_kernel(uint8_t *__restrict__ dq,
+                                                        uint16_t *__restrict__ ds,
+                                                        const int8_t *__restrict__ src,
+                                                        const uint16_t *__restrict__ ssrc,
+                                                        uint32_t n, uint32_t k) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kPanelRows * kRepackPitch];
+  const uint32_t p = blockIdx.x, cg = blockIdx.y, t = threadIdx.x;
+  const uint32_t R = panel_rows(n, p);
+  const uint32_t c0 = cg * kRepackChunks, nc = k / kChunkK;
+  const uint32_t chunks = nc - c0 < kRepackChunks ? nc - c0 : kRepackChunks;
+  const u32x4 flip = {0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u};
+  {
+    const uint32_t r = t >> 3, q = t & 7;  // 32 bytes per lane: columns 32q .. 32q + 31
+    if (r < R && q < 2 * chunks) {
+      const int8_t *row = src + (size_t)(p * kPanelRows + r) * k + c0 * kChunkK + q * 32;
+      u32x4 a = *reinterpret_cast<const u32x4 *>(row), b = *reinterpret_cast<const u32x4 *>(row + 16);
+      *reinterpret_cast<u32x4 *>(tile + r * kRepackPitch + q * 32) = a ^ flip;
+      *reinterpret_cast<u32x4 *>(tile + r * kRepackPitch + q * 32 + 16) = b ^ flip;
+    }
+    // scales: row r's blocks 8cg .. 8cg + 7
+    const uint32_t b = t & 7;
+    if (r < R && b < 2 * chunks) {
+      const uint32_t cl = b >> 1, h = b & 1;
+      ds[panel_chunk_sc(k, p, R, c0 + cl) + h * R + r] =
+          ssrc[(size_t)(p * kPanelRows + r) * (k / 32) + c0 * 2 + b];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    // unit v of the group in panel order: chunk cl, then (j, h) as 2j + h, then row r
+    const uint32_t v = t + 256 * i, cl = v >> 7, jh = (v >> 5) & 3, r = v & 31;
+    if (cl < chunks && r < R) {
+      const uint32_t j = jh >> 1, h = jh & 1;
+      *reinterpret_cast<u32x4 *>(dq + panel_chunk_qs(k, p, R, c0 + cl) + (jh * R + r) * 16) =
+          *reinterpret_cast<const u32x4 *>(tile + r * kRepackPitch + cl * kChunkK + h * 32 + j * 16);
+    }
+  }
 }
 
 static bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
@@ -131,15 +153,12 @@ extern "C" int madi_q8_repack(void *dst_qs, void *dst_scales, const void *qs, co
   if (!initialized()) return fail(MADI_ERR_NOT_INIT, "madi_q8_repack: madi_init has not succeeded");
   if (int rc = deferred_before_write(dst_qs, nq)) return rc;
   if (int rc = deferred_before_write(dst_scales, ns * 2)) return rc;
-  const size_t units = nq / 16;
-  hipLaunchKernelGGL(q8_repack_qs_kernel, dim3((unsigned)((units + 255) / 256)), dim3(256), 0,
-                     stream(), static_cast<uint8_t *>(dst_qs), static_cast<const int8_t *>(qs), n,
-                     k, units);
-  if (int rc = check_launch("madi_q8_repack(qs)")) return rc;
-  hipLaunchKernelGGL(q8_repack_sc_kernel, dim3((unsigned)((ns + 255) / 256)), dim3(256), 0,
-                     stream(), static_cast<uint16_t *>(dst_scales),
-                     static_cast<const uint16_t *>(scales), n, k, ns);
-  return check_launch("madi_q8_repack(scales)");
+  const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
+  const uint32_t groups = (k / kChunkK + kRepackChunks - 1) / kRepackChunks;
+  hipLaunchKernelGGL(q8_repack_kernel, dim3(np, groups), dim3(256), 0, stream(),
+                     static_cast<uint8_t *>(dst_qs), static_cast<uint16_t *>(dst_scales),
+                     static_cast<const int8_t *>(qs), static_cast<const uint16_t *>(scales), n, k);
+  return check_launch("madi_q8_repack");
 }
 
 // ------------------------------------------------------------------ quantise F16 -> panel Q8

@@ -101,7 +101,7 @@ def tile_rows(m):
 
 
 # ------------------------------------------------------------------ layout
-@pytest.mark.parametrize("n,k", [(64, 128), (100, 256), (51866, 1280)])
+@pytest.mark.parametrize("n,k", [(64, 128), (100, 256), (96, 320), (33, 192), (51866, 1280)])
 def test_device_repack_matches_host(q, n, k):
     say(f"repack n={n} k={k}")
     rng = np.random.default_rng(n)
