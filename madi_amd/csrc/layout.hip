@@ -96,6 +96,24 @@ extern "C" int madi_q8_unpack_host(void *dst_qs, void *dst_scales, const void *t
 constexpr uint32_t kRepackChunks = 4;
 constexpr uint32_t kRepackPitch = kRepackChunks * kChunkK + 16;  // LDS row bytes
 
+// The staged tile (row r's stored bytes q + 128 of chunks c0 .. c0 + chunks - 1
+// at r * kRepackPitch) out to panel p in the panel layout's own order: unit v
+// of the group is chunk v >> 7, then (j, h) as 2j + h, then row r, so
+// consecutive lanes write consecutive 16-byte units.
+__device__ inline void write_panel_units(uint8_t *__restrict__ dq, const uint8_t *tile, uint32_t k,
+                                         uint32_t p, uint32_t R, uint32_t c0, uint32_t chunks,
+                                         uint32_t t) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const uint32_t v = t + 256 * i, cl = v >> 7, jh = (v >> 5) & 3, r = v & 31;
+    if (cl < chunks && r < R) {
+      const uint32_t j = jh >> 1, h = jh & 1;
+      *reinterpret_cast<u32x4 *>(dq + panel_chunk_qs(k, p, R, c0 + cl) + (jh * R + r) * 16) =
+          *reinterpret_cast<const u32x4 *>(tile + r * kRepackPitch + cl * kChunkK + h * 32 + j * 16);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void q8_repack_kernel(uint8_t *__restrict__ dq,
                                                         uint16_t *__restrict__ ds,
                                                         const int8_t *__restrict__ src,
@@ -124,16 +142,7 @@ __global__ __launch_bounds__(256) void q8_repack_kernel(uint8_t *__restrict__ dq
     }
   }
   __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    // unit v of the group in panel order: chunk cl, then (j, h) as 2j + h, then row r
-    const uint32_t v = t + 256 * i, cl = v >> 7, jh = (v >> 5) & 3, r = v & 31;
-    if (cl < chunks && r < R) {
-      const uint32_t j = jh >> 1, h = jh & 1;
-      *reinterpret_cast<u32x4 *>(dq + panel_chunk_qs(k, p, R, c0 + cl) + (jh * R + r) * 16) =
-          *reinterpret_cast<const u32x4 *>(tile + r * kRepackPitch + cl * kChunkK + h * 32 + j * 16);
-    }
-  }
+  write_panel_units(dq, tile, k, p, R, c0, chunks, t);
 }
 
 static bool overlaps(const void *a, size_t na, const void *b, size_t nb) {
@@ -167,48 +176,58 @@ extern "C" int madi_q8_repack(void *dst_qs, void *dst_scales, const void *qs, co
 // (row, 32-block): scale = max|w| / 127 in f32 (1.0 for an all-zero block),
 // stored as f16; q = clamp(round_half_away(w * (1 / scale)), -127, 127), all
 // in correctly rounded f32 as the Zig loop does.
+// Grid (panels, ceil(K / 256)), as the repack: lane (r, b) of a workgroup
+// quantises row r's block b of four chunks (32 f16, 8 lanes per 512-byte row
+// segment), writes its scale to the panel position and its 32 stored bytes
+// to an LDS tile, from which the units leave in panel order.
 __global__ __launch_bounds__(256) void q8_quantize_kernel(uint8_t *__restrict__ dst_q,
                                                           uint16_t *__restrict__ dst_s,
                                                           const uint16_t *__restrict__ src,
-                                                          uint32_t n, uint32_t k, size_t blocks) {
-  const size_t u = (size_t)blockIdx.x * 256 + threadIdx.x;
-  if (u >= blocks) return;
-  const uint32_t nb = k / 32;
-  const uint32_t row = (uint32_t)(u / nb), b = (uint32_t)(u % nb);
-  const u32x4 *s4 = reinterpret_cast<const u32x4 *>(src + (size_t)row * k + (size_t)b * 32);
-  float w[32];
+                                                          uint32_t n, uint32_t k) {
+  __shared__ __attribute__((aligned(16))) uint8_t tile[kPanelRows * kRepackPitch];
+  const uint32_t p = blockIdx.x, cg = blockIdx.y, t = threadIdx.x;
+  const uint32_t R = panel_rows(n, p);
+  const uint32_t c0 = cg * kRepackChunks, nc = k / kChunkK;
+  const uint32_t chunks = nc - c0 < kRepackChunks ? nc - c0 : kRepackChunks;
+  const uint32_t r = t >> 3, b = t & 7;  // row r, block 8cg + b
+  if (r < R && b < 2 * chunks) {
+    const u32x4 *s4 = reinterpret_cast<const u32x4 *>(
+        src + (size_t)(p * kPanelRows + r) * k + (size_t)(c0 * 2 + b) * 32);
+    float w[32];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f16x8 v = __builtin_bit_cast(f16x8, s4[i]);
+    for (int i = 0; i < 4; ++i) {
+      const f16x8 v = __builtin_bit_cast(f16x8, s4[i]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) w[8 * i + e] = (float)v[e];
-  }
-  float mx = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    const float a = __builtin_fabsf(w[i]);
-    mx = a > mx ? a : mx;
-  }
-  const float scale = mx > 0.0f ? __fdiv_rn(mx, 127.0f) : 1.0f;
-  const float inv = __frcp_rn(scale);
-  uint32_t word[8];
-#pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    uint32_t packed = 0;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float q = roundf(__fmul_rn(w[4 * d + e], inv));
-      q = q < -127.0f ? -127.0f : (q > 127.0f ? 127.0f : q);
-      packed |= (uint32_t)((int)q + 128) << (8 * e);  // stored biased: q + 128
+      for (int e = 0; e < 8; ++e) w[8 * i + e] = (float)v[e];
     }
-    word[d] = packed;
+    float mx = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      const float a = __builtin_fabsf(w[i]);
+      mx = a > mx ? a : mx;
+    }
+    const float scale = mx > 0.0f ? __fdiv_rn(mx, 127.0f) : 1.0f;
+    const float inv = __frcp_rn(scale);
+    uint32_t word[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      uint32_t packed = 0;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float q = roundf(__fmul_rn(w[4 * d + e], inv));
+        q = q < -127.0f ? -127.0f : (q > 127.0f ? 127.0f : q);
+        packed |= (uint32_t)((int)q + 128) << (8 * e);  // stored biased: q + 128
+      }
+      word[d] = packed;
+    }
+    const uint32_t cl = b >> 1, h = b & 1;
+    uint8_t *row = tile + r * kRepackPitch + cl * kChunkK + h * 32;
+    *reinterpret_cast<u32x4 *>(row) = (u32x4){word[0], word[1], word[2], word[3]};
+    *reinterpret_cast<u32x4 *>(row + 16) = (u32x4){word[4], word[5], word[6], word[7]};
+    dst_s[panel_chunk_sc(k, p, R, c0 + cl) + h * R + r] = __builtin_bit_cast(uint16_t, (f16)scale);
   }
-  const uint32_t p = row / kPanelRows, r = row % kPanelRows, R = panel_rows(n, p);
-  const uint32_t c = b / 2, h = b % 2;
-  uint8_t *chunk = dst_q + panel_chunk_qs(k, p, R, c);
-  *reinterpret_cast<u32x4 *>(chunk + ((0 + h) * R + r) * 16) = (u32x4){word[0], word[1], word[2], word[3]};
-  *reinterpret_cast<u32x4 *>(chunk + ((2 + h) * R + r) * 16) = (u32x4){word[4], word[5], word[6], word[7]};
-  dst_s[panel_chunk_sc(k, p, R, c) + h * R + r] = __builtin_bit_cast(uint16_t, (f16)scale);
+  __syncthreads();
+  write_panel_units(dst_q, tile, k, p, R, c0, chunks, t);
 }
 
 extern "C" int madi_q8_quantize(void *dst_qs, void *dst_scales, const void *w_f16, uint32_t n,
@@ -221,9 +240,11 @@ extern "C" int madi_q8_quantize(void *dst_qs, void *dst_scales, const void *w_f1
   const size_t blocks = (size_t)n * (k / 32);
   if (int rc = deferred_before_write(dst_qs, (size_t)n * k)) return rc;
   if (int rc = deferred_before_write(dst_scales, blocks * 2)) return rc;
-  hipLaunchKernelGGL(q8_quantize_kernel, dim3((unsigned)((blocks + 255) / 256)), dim3(256), 0,
-                     stream(), static_cast<uint8_t *>(dst_qs), static_cast<uint16_t *>(dst_scales),
-                     static_cast<const uint16_t *>(w_f16), n, k, blocks);
+  const uint32_t np = (n + kPanelRows - 1) / kPanelRows;
+  const uint32_t groups = (k / kChunkK + kRepackChunks - 1) / kRepackChunks;
+  hipLaunchKernelGGL(q8_quantize_kernel, dim3(np, groups), dim3(256), 0, stream(),
+                     static_cast<uint8_t *>(dst_qs), static_cast<uint16_t *>(dst_scales),
+                     static_cast<const uint16_t *>(w_f16), n, k);
   return check_launch("madi_q8_quantize");
 }
 

@@ -984,7 +984,7 @@ def _knife_edge_weights(rng, n, k):
     return w
 
 
-@pytest.mark.parametrize("n,k", [(100, 256), (51866, 1280)])
+@pytest.mark.parametrize("n,k", [(100, 256), (96, 320), (33, 192), (51866, 1280)])
 def test_quantize_bit_exact(q, n, k):
     say(f"quantize n={n} k={k}")
     rng = np.random.default_rng(n)
