@@ -60,15 +60,22 @@ struct Plan {
 // is row 4i + lane/16, floats 4 * (lane % 16) .. +3 of the chunk (each load
 // instruction reads four whole 256-byte row segments).
 //
-// With f16 activations (H) the MFMA fragments come straight from memory: lane
-// (h, c) loads row c's 16 bytes of piece 4h + s for each k-step s (rows past
-// the slice's last row read zeros, outside the activation resource).
+// With f16 activations (H) and a full 32-row slice the MFMA fragments come
+// straight from memory: lane (h, c) loads row c's 16 bytes of piece 4h + s for
+// each k-step s.  For 8 or 16 rows most of those lanes would load rows past
+// the batch (zeros, outside the activation resource), so the rows are staged
+// instead, as the f32 ones: one coalesced 16-byte piece per lane and 8 rows
+// (piece lane % 8 of row lane / 8), copied into the wave's LDS tile and read
+// back as fragments.
+template <int XR, bool H>
+constexpr bool kStagedH = H && XR < 32;
+
 template <int P, int XR, bool H = false>
 struct Chunk {
   u32x4 w[P][2];
   uint32_t s[P];
   f32x4 x[H ? 1 : XR / 4];
-  u32x4 xh[H ? 4 : 1];
+  u32x4 xh[H ? (kStagedH<XR, H> ? XR / 8 : 4) : 1];
 };
 
 template <int P, int XR, bool H>
@@ -85,7 +92,12 @@ __device__ inline void load_weights(Chunk<P, XR, H> &b, const Plan<P> &pl, rsrc_
 }
 template <int P, int XR, bool H>
 __device__ inline void load_acts(Chunk<P, XR, H> &b, const Plan<P> &pl, rsrc_t xr, uint32_t c) {
-  if constexpr (H) {
+  if constexpr (kStagedH<XR, H>) {
+#pragma unroll
+    for (int i = 0; i < XR / 8; ++i)
+      b.xh[i] = __builtin_amdgcn_raw_buffer_load_b128(xr, pl.x_voff + i * 8 * pl.K * 2,
+                                                      c * kChunkK * 2, 0);
+  } else if constexpr (H) {
 #pragma unroll
     for (int s = 0; s < 4; ++s)
       b.xh[s] = __builtin_amdgcn_raw_buffer_load_b128(xr, pl.x_voff, c * kChunkK * 2 + s * 16, 0);
@@ -161,7 +173,12 @@ template <int P, int XR, bool H>
 __device__ inline void accumulate(const Chunk<P, XR, H> &b, uint8_t *xt, uint32_t lane,
                                   f32x16 (&acc)[P]) {
   f16x8 xf[4];
-  if constexpr (H) {
+  if constexpr (kStagedH<XR, H>) {
+#pragma unroll
+    for (int i = 0; i < XR / 8; ++i)
+      *reinterpret_cast<u32x4 *>(xt + x_piece(8 * i + (lane >> 3), lane & 7)) = b.xh[i];
+    read_frags<XR>(xt, lane, xf);
+  } else if constexpr (H) {
 #pragma unroll
     for (int s = 0; s < 4; ++s) xf[s] = __builtin_bit_cast(f16x8, b.xh[s]);
   } else {
@@ -239,7 +256,9 @@ __global__ __launch_bounds__(KW * 64) __attribute__((amdgpu_waves_per_eu(KW / 4 
   const uint32_t rows = M - m0 < kSlice ? M - m0 : kSlice;
   constexpr uint32_t xb = H ? 2 : 4;  // bytes per activation
   pl.xr = make_rsrc(static_cast<const uint8_t *>(x) + (size_t)m0 * K * xb, rows * K * xb);
-  pl.x_voff = H ? r * K * 2 + h * 64 : (lane >> 4) * K * 4 + (lane & 15) * 16;
+  pl.x_voff = kStagedH<XR, H> ? (lane >> 3) * K * 2 + (lane & 7) * 16
+             : H                ? r * K * 2 + h * 64
+                                : (lane >> 4) * K * 4 + (lane & 15) * 16;
 
   constexpr bool kStage = kStageWindow<P, KW, H>;
   uint8_t *xt = smem + wave * XR * 128 * (kStage ? WIN : 1);
