@@ -308,9 +308,12 @@ def config_encoder_window_engine(torch, stream, q8, reps=3):
 def config_batched_decode(torch, stream, q8, reps=20):
     """One batched decode step at M = 8 and 16 token rows: 4 decoder layers x
     (self q|k|v 1280->3840, self out, cross q, cross out 1280->1280, FFN
-    1280->5120->1280) + vocab 1280->51866 through the skinny Q8 projection, two
-    alternating weight sets (2 x 168 MB > the 256 MB Infinity Cache); plus the
-    per-chunk cross-attention K|V projection 1280->2560 at M = 1500 (GEMM)."""
+    1280->5120->1280) through the skinny Q8 projection (f32 rows, as proj
+    reaches it), then the vocab logits 1280->51866 as the engine issues them
+    (transcribe.zig:2391-2394: matmulF16Batched on deqW16's recorded copy of
+    the tied tok_emb, f16 rows in and out), two alternating weight sets
+    (2 x 168 MB > the 256 MB Infinity Cache); plus the per-chunk
+    cross-attention K|V projection 1280->2560 at M = 1500 (GEMM)."""
     from madi_amd import synth
     sets = []
     for s_ in range(2):
@@ -320,11 +323,21 @@ def config_batched_decode(torch, stream, q8, reps=20):
         sets.append((layers, vocab))
     xin = torch.from_numpy(np.random.default_rng(102).standard_normal((16, 5120)).astype(np.float32)).cuda()
     out = torch.empty((16, VOCAB), dtype=torch.float32, device="cuda")
+    # the logit step's operands: the f16 rows (bb_x16), deqW16's copy of each
+    # set's tok_emb (recorded, never written: the Q8 weight is what is read)
+    # and the f16 logits (bb_l16)
+    x16 = xin[:, :DIM].contiguous().half().view(torch.int16)
+    l16 = torch.empty((16, VOCAB), dtype=torch.int16, device="cuda")
+    temb = [torch.empty(VOCAB * DIM, dtype=torch.int16, device="cuda") for _ in sets]
+    for t16, (_, vocab) in zip(temb, sets):
+        q8.deqW16(t16, vocab, VOCAB, DIM)
     step_bytes = (DEC_LAYERS * sum(n * k + n * (k // 32) * 2 for _, n, k in DEC_SHAPES)
                   + VOCAB * DIM + VOCAB * (DIM // 32) * 2)
     res = {"workload": "batched decode step: 4 layers x (self qkv 1280->3840, self out, cross q, "
-                       "cross out 1280->1280, ffn 1280->5120->1280) + vocab 1280->51866, skinny "
-                       "Q8 projection, weights cold (two alternating sets)",
+                       "cross out 1280->1280, ffn 1280->5120->1280) through the skinny Q8 "
+                       "projection (f32 rows) + vocab 1280->51866 as the engine calls it "
+                       "(matmulF16Batched on deqW16's recorded tok_emb copy, f16 rows in and "
+                       "out), weights cold (two alternating sets)",
            "weight_bytes_per_step": step_bytes}
     from madi_amd.issue import IssueList
     for m in (8, 16):
@@ -334,7 +347,7 @@ def config_batched_decode(torch, stream, q8, reps=20):
             for ws in layers:
                 for j, (_, n, k) in enumerate(DEC_SHAPES):
                     q.pproj(xin, ws[j], out, m, n, k)
-            q.pproj(xin, vocab, out, m, VOCAB, DIM)
+            q.matmulF16Batched(x16, temb[i % 2], l16, m, VOCAB, DIM)
         step(0)
         step(1)
         tp = _timed(torch, stream, step, reps, settle=True)
@@ -343,7 +356,7 @@ def config_batched_decode(torch, stream, q8, reps=20):
         step(1, lst=two)
         t = _timed_list(torch, stream, two, reps // 2, per=2)
         byts = step_bytes + DEC_LAYERS * sum(m * k * 4 + m * n * 4 for _, n, k in DEC_SHAPES) \
-            + m * DIM * 4 + m * VOCAB * 4
+            + m * DIM * 2 + m * VOCAB * 2
         one = IssueList()   # one weight set every step (the engine's loop; warm)
         step(0, lst=one)
         tw = _timed_list(torch, stream, one, reps)
@@ -352,12 +365,16 @@ def config_batched_decode(torch, stream, q8, reps=20):
                         "issued_from": "C (madi_amd.issue)",
                         "python_issued_us_per_step": round(tp * 1e6, 2),
                         "warm_us_per_step": round(tw * 1e6, 2)}
-        tv = _timed(torch, stream, lambda i, m=m: q8.pproj(xin, sets[i % 2][1], out, m, VOCAB, DIM),
-                    reps)
-        vb = VOCAB * DIM + VOCAB * (DIM // 32) * 2 + m * DIM * 4 + m * VOCAB * 4
+        tv = _timed(torch, stream,
+                    lambda i, m=m: q8.matmulF16Batched(x16, temb[i % 2], l16, m, VOCAB, DIM), reps)
+        vb = VOCAB * DIM + VOCAB * (DIM // 32) * 2 + m * DIM * 2 + m * VOCAB * 2
         res[f"m{m}"]["vocab_us"] = round(tv * 1e6, 2)
         res[f"m{m}"]["vocab_frac_hbm_peak"] = round(vb / tv / 1e9 / PEAK_HBM_GBS, 4)
-    del sets
+    # the copies were only recorded: drop the records before torch reuses
+    # their memory (madi_q8_forget writes nothing)
+    for t16 in temb:
+        q8.forget(t16)
+    del sets, temb
     m = 1500
     ctx = torch.from_numpy(synth.activations(np.random.default_rng(103), m, DIM).view(np.int16)).cuda()
     kv = torch.empty((m, 2560), dtype=torch.int16, device="cuda")
