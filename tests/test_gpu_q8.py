@@ -1078,6 +1078,76 @@ def test_f16_gemm_kM4_epilogues(q, epi):
     assert normwise(got, ref) <= TOL
 
 
+# kM4 / kM4Bias on true F16 weights (the encoder's F16 cache) through the
+# hand-written NN GEMM: each tile shape (128 x 256 from 160 tiles, else
+# 128 x 128, else 64 x 128), ragged row counts, K loops shorter than the LDS
+# ring (1 and 3 chunks) and fc2's 80 chunks, the encoder's M = 1500 shapes
+NN_CASES = [
+    (1500, 5120, 1280, O.EPI_BIAS_GELU),  # fc1: 128 x 256 tiles
+    (1000, 5120, 1280, O.EPI_NONE),       # 128 x 256, last tile 104 rows
+    (1500, 5120, 64, O.EPI_BIAS),         # 128 x 256, one chunk
+    (1500, 2560, 1280, O.EPI_NONE),       # cross K|V: 128 x 128 tiles
+    (1500, 1280, 1280, O.EPI_BIAS),       # q, k, v, out: 64 x 128 tiles
+    (1500, 1280, 5120, O.EPI_NONE),       # fc2: 64 x 128, 80 chunks
+    (65, 384, 192, O.EPI_BIAS_GELU),      # three chunks, 65 rows
+    (1, 128, 64, O.EPI_BIAS),             # one row, one chunk
+]
+
+
+@pytest.mark.parametrize("m,n,k,epi", NN_CASES)
+def test_f16_nn_gemm(q, m, n, k, epi):
+    """The F16-weight GEMM with the reference's epilogue order (the product
+    rounded to f16, then + bias, GELU, rounded again; m4_gemm.metal:79-85,
+    108-114) against the oracle's f16 GEMM on rows over every 32- and 64-row
+    boundary: element-wise within fp32 accumulation + one f16 rounding of the
+    exact product (no epilogue), normwise within the path's tolerance of the
+    composed oracle (with one)."""
+    say(f"f16 NN GEMM m={m} n={n} k={k} epi={epi}")
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    b = (rng.standard_normal((k, n)) * 0.05).astype(np.float16)
+    bias = rng.standard_normal(n).astype(np.float32)
+    dc = torch.full((m, n), -1, dtype=torch.int16, device="cuda")
+    if epi == O.EPI_NONE:
+        q.kM4("m4_gemm_nn", dev_f16(a), dev_f16(b), dc, m, n, k)
+    else:
+        q.kM4Bias("m4_gemm_bias_gelu" if epi == O.EPI_BIAS_GELU else "m4_gemm_bias",
+                  dev_f16(a), dev_f16(b), dc, dev(bias), m, n, k)
+    q.sync()
+    rows = np.unique(np.r_[0, 1, 31, 32, 63, 64, 127, 128, 255, 256, m // 2, m - 2, m - 1])
+    rows = rows[(rows >= 0) & (rows < m)]
+    got = host_f16(dc)[rows].astype(np.float64)
+    c16 = O.gemm_f16(a[rows], b, threads=8)
+    if epi == O.EPI_NONE:
+        exact = a[rows].astype(np.float64) @ b.astype(np.float64)
+        bound = 2.0**-11 * np.abs(exact) + (k + 2) * 2.0**-24 * (
+            np.abs(a[rows].astype(np.float64)) @ np.abs(b.astype(np.float64))) + 2.0**-24
+        assert np.all(np.abs(got - exact) <= bound * 1.001)
+        ref = c16.astype(np.float64)
+    else:
+        v = c16.astype(np.float32) + bias[None, :]
+        if epi == O.EPI_BIAS_GELU:
+            v = np.vectorize(O.gelu_erf, otypes=[np.float32])(v)
+        ref = O.f32_to_f16(v).astype(np.float64)
+    assert normwise(got, ref) <= TOL
+
+
+def test_f16_nn_gemm_leaves_other_rows(q):
+    """Rows past M are never written (the last tile's clamped rows are read,
+    not stored): the output sits inside a taller sentinel buffer."""
+    m, n, k = 70, 256, 128
+    rng = np.random.default_rng(90)
+    a = rng.standard_normal((m, k)).astype(np.float16)
+    b = (rng.standard_normal((k, n)) * 0.05).astype(np.float16)
+    big = torch.full((m + 64, n), 0x7E00, dtype=torch.int16, device="cuda")
+    q.kM4("m4_gemm_nn", dev_f16(a), dev_f16(b), big, m, n, k)
+    q.sync()
+    out = big.cpu().numpy()
+    assert np.all(out[m:] == 0x7E00)
+    assert normwise(out[:m].view(np.float16).astype(np.float64),
+                    O.gemm_f16(a, b, threads=8).astype(np.float64)) <= TOL
+
+
 def test_stream_switch_orders_split_k(q):
     """madi_set_stream makes the new stream wait for the work already issued
     on the old one.  Split-K launches (the FFN-down GEMV 5120 -> 1280, four K
