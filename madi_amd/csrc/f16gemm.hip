@@ -10,18 +10,20 @@
 // A[M][K] . B[K][N], all f16 row-major, fp32 accumulation, and the
 // reference's epilogue in the same kernel (the product rounded to f16, then
 // the f32 bias added and GELU applied, rounded again: m4_gemm.metal:79-85,
-// 108-114).  Four waves per workgroup; each chunk of 64 k brings the A tile
-// (BM rows x 128 bytes) and the B tile (64 rows x BN columns) into an LDS
-// ring by LDS DMA, one barrier per chunk.  The A fragments are 16-byte LDS
-// reads of a row; the B operand needs eight consecutive k of one column,
-// which the row-major B tile gives through the transpose read
+// 108-114).  Each chunk of 64 k brings the A tile (BM rows x 128 bytes) and
+// the B tile (64 rows x BN columns) into an LDS ring by LDS DMA, issued by
+// four producer waves while four computing waves (one per SIMD each) read
+// fragments and run the MFMAs; one barrier per chunk.  The A fragments are
+// 16-byte LDS reads of a row; the B operand needs eight consecutive k of one
+// column, which the row-major B tile gives through the transpose read
 // (ds_read_b64_tr_b16: 16 lanes pass 4 rows x 16 columns, lane c receives
 // column c's 4 values), two per fragment.  The MFMA takes the B fragment as
-// its first operand, so each lane accumulates C^T: four consecutive columns
-// of one row, stored as one 8-byte piece.  Shapes the kernel does not take
-// (K not a multiple of 64, N not a multiple of 128, misaligned rows), and
-// matmulF16Batched with alpha != 1 or beta != 0, run rocBLAS gemm_ex with
-// fp32 accumulation; its bias epilogue is then an elementwise pass.
+// its first operand, so each lane accumulates C^T (four consecutive columns
+// of one row); the finished tile goes through LDS and leaves as whole rows.
+// Shapes the kernel does not take (K not a multiple of 64, N not a multiple
+// of 128, misaligned rows), and matmulF16Batched with alpha != 1 or
+// beta != 0, run rocBLAS gemm_ex with fp32 accumulation; its bias epilogue
+// is then an elementwise pass.
 #include <rocblas/rocblas.h>
 
 #include "common.h"
@@ -58,6 +60,7 @@ using NnSmall = NnGeom<1, 2, 2, 2>;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+typedef __attribute__((address_space(3))) u32x2 lds_u32x2;
 __device__ inline f16x8 lds_read16(uint32_t addr) {
   return __builtin_bit_cast(f16x8, *(const lds_u32x4 *)(uintptr_t)addr);
 }
@@ -80,13 +83,23 @@ __device__ inline uint32_t swz_b(uint32_t row) { return (row & 3) << 2; }
 // columns of a run are fetched into one L2.  M rows past the last are read
 // as the last row (in bounds) and never stored.  Requires K % 64 == 0,
 // N % BN == 0, A, B, C and bias 16-byte aligned.
+//
+// Eight waves, two per SIMD: waves 0-3 compute (fragment reads and MFMAs),
+// waves 4-7 only issue the LDS DMAs.  A DMA waits for room in the address
+// queue at issue; in a computing wave that wait would hold back its MFMAs,
+// here it holds back only the producing wave while the other wave of its
+// SIMD keeps the matrix pipe busy.  Both kinds of wave meet at one barrier
+// per chunk: the producers arrive once their DMAs of the chunk about to be
+// computed have landed (vmcnt), the computing waves once they are done
+// reading the chunk before, whose stage the producers refill right after.
 template <class G, int EPI>
-__global__ __launch_bounds__(256) void f16_nn_gemm_kernel(
+__global__ __launch_bounds__(512) void f16_nn_gemm_kernel(
     const f16 *__restrict__ A, const f16 *__restrict__ B, uint32_t M, uint32_t N, uint32_t K,
     uint32_t tiles_m, uint32_t tiles, f16 *__restrict__ C, const float *__restrict__ bias) {
   constexpr int S = G::kStages, BN = G::BN, TMw = G::kTM, TNw = G::kTN, WNw = G::kWN;
   __shared__ __attribute__((aligned(1024))) uint8_t smem[S * G::kStage];
-  const uint32_t lane = threadIdx.x & 63, wave = sgpr(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63, wave8 = sgpr(threadIdx.x >> 6);
+  const uint32_t wave = wave8 & 3;
   const uint32_t h = lane >> 5, r = lane & 31;
 
   const uint32_t b = blockIdx.x, x = b & 7, per = tiles >> 3, extra = tiles & 7;
@@ -95,125 +108,150 @@ __global__ __launch_bounds__(256) void f16_nn_gemm_kernel(
   const uint32_t item = x * per + (x < extra ? x : extra) + slot;
   const uint32_t tn = item / tiles_m, tm = item - tn * tiles_m;
   const uint32_t m0 = tm * G::BM, n0 = tn * BN, nk = K / 64;
-
-  // DMA plan.  A: DMA j copies rows 8j .. 8j+7 of the tile, lane -> row
-  // 8j + lane/8 at stored piece lane%8.  B: DMA j copies stored pieces
-  // 64j .. 64j+63 of the row-major tile (BN/8 per row).
-  const desc_t da = make_desc(A, M * K * 2), db = make_desc(B, K * N * 2);
-  const desc_t dz = make_desc(A, 0);
-  uint32_t va[G::kDA], vb[G::kDB];
-#pragma unroll
-  for (int i = 0; i < G::kDA; ++i) {
-    const uint32_t row = 8 * (wave * G::kDA + i) + (lane >> 3);
-    const uint32_t gr = m0 + row < M ? m0 + row : M - 1;
-    va[i] = gr * K * 2 + 16 * ((lane & 7) ^ swz_a(row));
-  }
-#pragma unroll
-  for (int i = 0; i < G::kDB; ++i) {
-    const uint32_t s = 64 * (wave * G::kDB + i) + lane;
-    const uint32_t row = s / (BN / 8), q = s % (BN / 8);
-    vb[i] = row * N * 2 + 2 * n0 + 16 * (q ^ swz_b(row));
-  }
   const uint32_t ring = lds_addr(smem);
-  // chunk c into stage st; chunks past the last load through an empty
-  // descriptor (zeros into a stage no later chunk reads), so every trip
-  // issues the same DMAs and one wait count serves every trip
-  auto issue = [&](uint32_t c, uint32_t st) {
-    const uint32_t base = ring + st * G::kStage;
-    const bool real = c < nk;
-    const desc_t a_ = real ? da : dz, b_ = real ? db : dz;
-    const uint32_t ca = real ? c * 128 : 0, cb = real ? c * 128 * N : 0;
-#pragma unroll
-    for (int i = 0; i < G::kDA; ++i) dma16<0, true>(a_, va[i], ca, base + 1024 * (wave * G::kDA + i));
-#pragma unroll
-    for (int i = 0; i < G::kDB; ++i)
-      dma16<0, true>(b_, vb[i], cb, base + G::kABytes + 1024 * (wave * G::kDB + i));
-  };
+  constexpr uint32_t kPieces = BN / 8;  // 16-byte pieces per tile row
 
-  // fragment addresses.  Wave (wm, wn) owns rows 32*TMw*wm .. and columns
-  // 32*TNw*wn .. of the tile.
-  const uint32_t wm = wave / WNw, wn = wave % WNw;
-  // A: row 32*TMw*wm + 32*i + r at piece (2*ks + h) ^ swz_a(r)
-  const uint32_t a_lane = (32 * TMw * wm + r) * 128;
-  const uint32_t sa_r = swz_a(r);
-  // B: lane (h, xh, c16) passes row 16*ks + 8*h + c16/4 (+4 for the second
-  // half of the fragment), columns 32*TNw*wn + 32*j + 16*xh + 4*(c16%4) .. +3
-  const uint32_t c16 = lane & 15, xh = (lane >> 4) & 1;
-  const uint32_t b_lane = (8 * h + (c16 >> 2)) * (BN * 2) + 8 * (c16 & 1);
-  const uint32_t b_p0 = 4 * TNw * wn + 2 * xh + ((c16 & 3) >> 1), b_sw = swz_b(c16 >> 2);
-
-  f32x16 acc[TMw][TNw];
+  if (wave8 >= 4) {
+    // ---- producer wave `wave`.  A: DMA j copies rows 8j .. 8j+7 of the
+    // tile, lane -> row 8j + lane/8 at stored piece lane%8.  B: DMA j copies
+    // stored pieces 64j .. 64j+63 of the row-major tile (BN/8 per row).
+    const desc_t da = make_desc(A, M * K * 2), db = make_desc(B, K * N * 2);
+    const desc_t dz = make_desc(A, 0);
+    uint32_t va[G::kDA], vb[G::kDB];
 #pragma unroll
-  for (int i = 0; i < TMw; ++i)
+    for (int i = 0; i < G::kDA; ++i) {
+      const uint32_t row = 8 * (wave * G::kDA + i) + (lane >> 3);
+      const uint32_t gr = m0 + row < M ? m0 + row : M - 1;
+      va[i] = gr * K * 2 + 16 * ((lane & 7) ^ swz_a(row));
+    }
 #pragma unroll
-    for (int j = 0; j < TNw; ++j) acc[i][j] = (f32x16){};
-
+    for (int i = 0; i < G::kDB; ++i) {
+      const uint32_t s = 64 * (wave * G::kDB + i) + lane;
+      const uint32_t row = s / (BN / 8), q = s % (BN / 8);
+      vb[i] = row * N * 2 + 2 * n0 + 16 * (q ^ swz_b(row));
+    }
+    // chunk c into stage st; chunks past the last load through an empty
+    // descriptor (zeros into a stage no later chunk reads), so every trip
+    // issues the same DMAs and one wait count serves every trip
+    auto issue = [&](uint32_t c, uint32_t st) {
+      const uint32_t base = ring + st * G::kStage;
+      const bool real = c < nk;
+      const desc_t a_ = real ? da : dz, b_ = real ? db : dz;
+      const uint32_t ca = real ? c * 128 : 0, cb = real ? c * 128 * N : 0;
 #pragma unroll
-  for (int s = 0; s < S - 1; ++s) issue(s, s);
-  uint32_t st = 0;
+      for (int i = 0; i < G::kDA; ++i) dma16<0, true>(a_, va[i], ca, base + 1024 * (wave * G::kDA + i));
+#pragma unroll
+      for (int i = 0; i < G::kDB; ++i)
+        dma16<0, true>(b_, vb[i], cb, base + G::kABytes + 1024 * (wave * G::kDB + i));
+    };
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) issue(s, s);
+    uint32_t st = 0;
 #pragma unroll 1
-  for (uint32_t c = 0; c < nk; ++c) {
-    wait_then_barrier<(S - 2) * G::kD>();
-    issue(c + S - 1, st == 0 ? S - 1 : st - 1);
-    const uint32_t sa = ring + st * G::kStage, sb = sa + G::kABytes;
-    // k-step ks's fragments into slot ks & 1: read one k-step ahead of the
-    // MFMAs that use them
-    f16x8 af[2][TMw], bf[2][TNw];
-    auto read = [&](int ks) {
+    for (uint32_t c = 0; c < nk; ++c) {
+      wait_then_barrier<(S - 2) * G::kD>();
+      issue(c + S - 1, st == 0 ? S - 1 : st - 1);
+      st = st == S - 1 ? 0 : st + 1;
+    }
+    wait_then_barrier<0>();  // every DMA has landed: the ring is free
+    wait_then_barrier<0>();  // the tile is staged
+  } else {
+    // ---- computing wave (wm, wn): rows 32*TMw*wm .. and columns 32*TNw*wn ..
+    // of the tile.  A: row 32*TMw*wm + 32*i + r at piece (2*ks + h) ^ swz_a(r).
+    // B: lane (h, xh, c16) passes row 16*ks + 8*h + c16/4 (+4 for the second
+    // half of the fragment), columns 32*TNw*wn + 32*j + 16*xh + 4*(c16%4) .. +3
+    const uint32_t wm = wave / WNw, wn = wave % WNw;
+    const uint32_t a_lane = (32 * TMw * wm + r) * 128;
+    const uint32_t sa_r = swz_a(r);
+    const uint32_t c16 = lane & 15, xh = (lane >> 4) & 1;
+    const uint32_t b_lane = (8 * h + (c16 >> 2)) * (BN * 2) + 8 * (c16 & 1);
+    const uint32_t b_p0 = 4 * TNw * wn + 2 * xh + ((c16 & 3) >> 1), b_sw = swz_b(c16 >> 2);
+
+    f32x16 acc[TMw][TNw];
 #pragma unroll
-      for (int i = 0; i < TMw; ++i)
-        af[ks & 1][i] = lds_read16(sa + a_lane + 32 * 128 * i + 16 * ((2 * ks + h) ^ sa_r));
+    for (int i = 0; i < TMw; ++i)
+#pragma unroll
+      for (int j = 0; j < TNw; ++j) acc[i][j] = (f32x16){};
+
+    uint32_t st = 0;
+#pragma unroll 1
+    for (uint32_t c = 0; c < nk; ++c) {
+      wait_then_barrier<0>();  // chunk c has landed; chunk c-1's stage is free
+      const uint32_t sa = ring + st * G::kStage, sb = sa + G::kABytes;
+      // k-step ks's fragments into slot ks & 1: read one k-step ahead of the
+      // MFMAs that use them
+      f16x8 af[2][TMw], bf[2][TNw];
+      auto read = [&](int ks) {
+#pragma unroll
+        for (int i = 0; i < TMw; ++i)
+          af[ks & 1][i] = lds_read16(sa + a_lane + 32 * 128 * i + 16 * ((2 * ks + h) ^ sa_r));
+#pragma unroll
+        for (int j = 0; j < TNw; ++j) {
+          const uint32_t at = sb + 16 * ks * BN * 2 + b_lane + 16 * ((b_p0 + 4 * j) ^ b_sw);
+          const f16x4 lo = lds_read_tr(at), hi = lds_read_tr(at + 4 * BN * 2);
+          bf[ks & 1][j] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+      };
+      read(0);
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        // the next k-step's reads stay ahead of this k-step's MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks < 3) read(ks + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < TMw; ++i)
+#pragma unroll
+          for (int j = 0; j < TNw; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[ks & 1][j], af[ks & 1][i], acc[i][j], 0, 0, 0);
+      }
+      st = st == S - 1 ? 0 : st + 1;
+    }
+
+    // Epilogue.  acc[i][j][4q + e] is the tile's element (row, col), row =
+    // 32*TMw*wm + 32*i + r, col = 32*TNw*wn + 32*j + 8*q + 4*h + e: bias and
+    // GELU in registers, then the tile through LDS (free once every DMA has
+    // landed and every fragment read is done), so that C leaves as whole rows
+    // of 16-byte pieces; written straight from the MFMA layout, each store
+    // would touch 32 rows with 8 bytes.  Row t of the staged tile keeps its
+    // logical 16-byte piece p at p ^ (t & 15): the 8-byte writes of 32 rows
+    // at one piece, and the 16-byte reads of whole rows, spread over all banks.
+    wait_then_barrier<0>();
+#pragma unroll
+    for (int i = 0; i < TMw; ++i) {
+      const uint32_t trow = 32 * TMw * wm + 32 * i + r;
+      const uint32_t rowb = ring + trow * (BN * 2), sw = trow & 15;
 #pragma unroll
       for (int j = 0; j < TNw; ++j) {
-        const uint32_t at = sb + 16 * ks * BN * 2 + b_lane + 16 * ((b_p0 + 4 * j) ^ b_sw);
-        const f16x4 lo = lds_read_tr(at), hi = lds_read_tr(at + 4 * BN * 2);
-        bf[ks & 1][j] = (f16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      }
-    };
-    read(0);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      // the next k-step's reads stay ahead of this k-step's MFMAs
-      __builtin_amdgcn_sched_barrier(0);
-      if (ks < 3) read(ks + 1);
-      __builtin_amdgcn_sched_barrier(0);
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t tcol = 32 * TNw * wn + 32 * j + 8 * q + 4 * h;
+          f16x4 o;
+          if constexpr (EPI == MADI_EPI_NONE) {
 #pragma unroll
-      for (int i = 0; i < TMw; ++i)
+            for (int e = 0; e < 4; ++e) o[e] = (f16)acc[i][j][4 * q + e];
+          } else {
+            const f32x4 bv = *reinterpret_cast<const f32x4 *>(bias + n0 + tcol);
 #pragma unroll
-        for (int j = 0; j < TNw; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[ks & 1][j], af[ks & 1][i], acc[i][j], 0, 0, 0);
-    }
-    st = st == S - 1 ? 0 : st + 1;
-  }
-  // the trailing empty DMAs land before the workgroup can end
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-
-  // epilogue: acc[i][j][4q + e] is C[row][col], row = m0 + 32*TMw*wm + 32*i + r,
-  // col = n0 + 32*TNw*wn + 32*j + 8*q + 4*h + e
-#pragma unroll
-  for (int i = 0; i < TMw; ++i) {
-    const uint32_t row = m0 + 32 * TMw * wm + 32 * i + r;
-#pragma unroll
-    for (int j = 0; j < TNw; ++j) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const uint32_t col = n0 + 32 * TNw * wn + 32 * j + 8 * q + 4 * h;
-        f16x4 o;
-        if constexpr (EPI == MADI_EPI_NONE) {
-#pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = (f16)acc[i][j][4 * q + e];
-        } else {
-          const f32x4 bv = *reinterpret_cast<const f32x4 *>(bias + col);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float v = (float)(f16)acc[i][j][4 * q + e] + bv[e];
-            if constexpr (EPI == MADI_EPI_BIAS_GELU) v = gelu_erf_fast(v);
-            o[e] = (f16)v;
+            for (int e = 0; e < 4; ++e) {
+              float v = (float)(f16)acc[i][j][4 * q + e] + bv[e];
+              if constexpr (EPI == MADI_EPI_BIAS_GELU) v = gelu_erf_fast(v);
+              o[e] = (f16)v;
+            }
           }
+          *(lds_u32x2 *)(uintptr_t)(rowb + 16 * ((tcol >> 3) ^ sw) + 8 * h) = __builtin_bit_cast(u32x2, o);
         }
-        if (row < M) *reinterpret_cast<f16x4 *>(C + (size_t)row * N + col) = o;
       }
     }
+    wait_then_barrier<0>();
+  }
+  // all eight waves store: thread t takes piece (512 s + t) of the tile in
+  // row-major order
+#pragma unroll
+  for (uint32_t s = 0; s < G::BM * kPieces / 512; ++s) {
+    const uint32_t e = 512 * s + threadIdx.x, trow = e / kPieces, p = e % kPieces;
+    const u32x4 v = *(const lds_u32x4 *)(uintptr_t)(ring + trow * (BN * 2) + 16 * (p ^ (trow & 15)));
+    if (m0 + trow < M) *reinterpret_cast<u32x4 *>(C + (size_t)(m0 + trow) * N + n0 + 8 * p) = v;
   }
 }
 rocblas_handle g_blas = nullptr;
@@ -305,7 +343,7 @@ template <class G, int EPI>
 int launch_nn(const void *a, const void *b, void *c, const float *bias, uint32_t m, uint32_t n,
               uint32_t k, const char *what) {
   const uint32_t tiles_m = (m + G::BM - 1) / G::BM, tiles = tiles_m * (n / G::BN);
-  hipLaunchKernelGGL((f16_nn_gemm_kernel<G, EPI>), dim3((tiles + 7) & ~7u), dim3(256), 0, stream(),
+  hipLaunchKernelGGL((f16_nn_gemm_kernel<G, EPI>), dim3((tiles + 7) & ~7u), dim3(512), 0, stream(),
                      static_cast<const f16 *>(a), static_cast<const f16 *>(b), m, n, k, tiles_m,
                      tiles, static_cast<f16 *>(c), bias);
   return check_launch(what);
