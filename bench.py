@@ -26,8 +26,9 @@ call sequence issued from compiled code (madi_amd.issue, a C loop over the
 library's calls, as the engine issues from Zig): the encoder GEMM set of one
 30 s window (32 layers, independent weights) with q|k|v stacked, and the same
 window as the engine's layer loop issues it (q, k, v through kDeq + kM4Bias on
-slices of the stacked weight, grouped into one launch at the boundary), a
-batched decode step at M = 8 and 16 (skinny Q8 projections, cold weights) with
+slices of the stacked weight, grouped into one launch at the boundary) and in
+its F16-cache mode (kM4 / kM4Bias on true F16 weights through the NN f16
+GEMM), a batched decode step at M = 8 and 16 (skinny Q8 projections, cold weights) with
 the per-chunk cross-attention K|V GEMM, one decoder token at M = 1 through the
 GEMV family (and its fused q|k|v GEMV alone), one decoder layer's sequence
 prefill projections at M = 320, the 16-window long-audio fc1/fc2, and the
@@ -299,6 +300,52 @@ def config_encoder_window_engine(torch, stream, q8, reps=3):
                     "encoder.zig:256-303 issues them (kDeq + kM4/kM4Bias handles through the "
                     "deferred dequantisation, q|k|v grouped into one launch), independent "
                     "weights per layer, issued from C",
+        "ms_per_window": round(t * 1e3, 4), "tflop_per_window": round(flops / 1e12, 4),
+        "tflops": round(flops / t / 1e12, 1),
+        "frac_fp16_peak": round(flops / t / 1e12 / PEAK_FP16_TFLOPS, 4),
+    }
+
+
+def config_encoder_window_f16cache(torch, stream, q8, reps=3):
+    """The encoder window in the engine's F16-cache mode (ENC_F16_CACHE,
+    transcribe.zig:1149): every projection holds a true F16 weight [K][N]
+    (L.q_f16 .. L.m2_f16) and encoder.zig:262-301 calls kM4 / kM4Bias on it
+    with no kDeq: q, k, v 1280->1280 + bias, out 1280->1280, fc1 1280->5120 +
+    bias + GELU, fc2 5120->1280.  32 layers, independent weights (1.26 GB of
+    F16), M = 1500, issued from C through madi_m4_gemm (the NN f16 GEMM)."""
+    from madi_amd.issue import IssueList
+    m, d, mlp = 1500, DIM, 5120
+    g = torch.Generator(device="cuda").manual_seed(111)
+    f16 = lambda *shape, s=1.0: (torch.randn(shape, generator=g, device="cuda") * s).half()
+    x_ln, ao, x_ln2 = f16(m, d), f16(m, d), f16(m, d)
+    qkv = torch.empty((3, m, d), dtype=torch.half, device="cuda")
+    mo = torch.empty((m, d), dtype=torch.half, device="cuda")
+    mh = torch.empty((m, mlp), dtype=torch.half, device="cuda")
+    m4, m4b, m4bg = (q8.getFunction(nm) for nm in ("m4_gemm_nn", "m4_gemm_bias", "m4_gemm_bias_gelu"))
+    layers = []
+    for _ in range(ENC_LAYERS):
+        layers.append(dict(q=f16(d, d, s=0.03), k=f16(d, d, s=0.03), v=f16(d, d, s=0.03),
+                           o=f16(d, d, s=0.03), m0=f16(d, mlp, s=0.03), m2=f16(mlp, d, s=0.015),
+                           qb=torch.randn(d, generator=g, device="cuda"),
+                           kb=torch.randn(d, generator=g, device="cuda"),
+                           vb=torch.randn(d, generator=g, device="cuda"),
+                           m0b=torch.randn(mlp, generator=g, device="cuda")))
+    torch.cuda.synchronize()
+    window = IssueList()
+    for L in layers:
+        for w, bias_, out in ((L["q"], L["qb"], qkv[0]), (L["k"], L["kb"], qkv[1]), (L["v"], L["vb"], qkv[2])):
+            window.kM4Bias(m4b, x_ln, w, out, bias_, m, d, d)
+        window.kM4(m4, ao, L["o"], mo, m, d, d)
+        window.kM4Bias(m4bg, x_ln2, L["m0"], mh, L["m0b"], m, mlp, d)
+        window.kM4(m4, mh, L["m2"], mo, m, d, mlp)
+    t = _timed_list(torch, stream, window, reps)
+    flops = ENC_LAYERS * 2.0 * m * (4 * d * d + 2 * d * mlp)
+    del layers
+    return {
+        "workload": "32 layers x (q, k, v 1280->1280 +bias, out 1280->1280, fc1 1280->5120 "
+                    "+bias+GELU, fc2 5120->1280) at M=1500 on true F16 weights [K][N], as "
+                    "encoder.zig:262-301 issues them in the F16-cache mode (kM4 / kM4Bias, no "
+                    "kDeq), independent weights per layer, issued from C",
         "ms_per_window": round(t * 1e3, 4), "tflop_per_window": round(flops / 1e12, 4),
         "tflops": round(flops / t / 1e12, 1),
         "frac_fp16_peak": round(flops / t / 1e12 / PEAK_FP16_TFLOPS, 4),
@@ -599,7 +646,8 @@ def config_encoder_attention(torch, stream, q8, reps=50):
 
 CONFIGS = {
     "encoder_window": config_encoder_window,
-    "encoder_window_engine": config_encoder_window_engine, "batched_decode": config_batched_decode,
+    "encoder_window_engine": config_encoder_window_engine,
+    "encoder_window_f16cache": config_encoder_window_f16cache, "batched_decode": config_batched_decode,
     "decode_token": config_decode_token, "prefill": config_prefill,
     "long_audio": config_long_audio, "encoder_attention": config_encoder_attention,
 }
@@ -756,6 +804,8 @@ def main():
         cfg = {"encoder_window": config_encoder_window(torch, stream, q8)}
         log("encoder window as the engine issues it (32 layers x 6 GEMMs at M=1500)")
         cfg["encoder_window_engine"] = config_encoder_window_engine(torch, stream, q8)
+        log("encoder window in the F16-cache mode (32 layers x 6 GEMMs on F16 weights)")
+        cfg["encoder_window_f16cache"] = config_encoder_window_f16cache(torch, stream, q8)
         log("batched decode (M=8, 16)")
         cfg["batched_decode"] = config_batched_decode(torch, stream, q8)
         log("decoder token (M=1, GEMV family)")
