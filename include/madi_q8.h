@@ -276,18 +276,21 @@ int madi_set_deferred_dequant(int on);
  * (which launches a held group).  No counterpart in the reference. */
 int madi_set_gemm_grouping(int on);
 
-/* ---- plain fp16 GEMMs (pre-dequantised F16 weights) ------------------------ */
+/* ---- fp16 GEMMs (pre-dequantised F16 weights) ------------------------------ */
 /* C[M][N] (f16) = epi(A[M][K] (f16) . B[K][N] (f16)), all row-major, fp32
  * accumulation.  Replaces kM4 / kM4Bias (engine/metal/encoder.zig:125-136) ->
  * m4_gemm_nn / m4_gemm_bias / m4_gemm_bias_gelu (kernels/m4_gemm.metal:19-115)
  * for callers that hold an F16 weight in the [K][N] layout kDeq produces.
  * Epilogues round like the reference: c = f16(A.B), then f16(c + bias[n]) and
- * for BIAS_GELU f16(gelu(c + bias[n])).  Runs as a library GEMM (rocBLAS). */
+ * for BIAS_GELU f16(gelu(c + bias[n])).  K a multiple of 64, N of 128 and
+ * 16-byte aligned a, b, c and bias run the library's NN f16 GEMM (epilogue in
+ * the kernel); other shapes run rocBLAS and an elementwise epilogue pass. */
 int madi_f16_gemm(const void *a, const void *b, void *c, const float *bias, uint32_t m,
                   uint32_t n, uint32_t k, int epilogue);
 /* C = alpha * A . B + beta * C, f16 row-major [M][K] . [K][N] -> [M][N], fp32
  * accumulation.  Replaces mtl_matmul_f16_enc (engine/metal/metal_backend.h:103),
- * behind matmulF16Batched (metal_backend.zig:120). */
+ * behind matmulF16Batched (metal_backend.zig:120).  alpha 1 and beta 0 on the
+ * shapes madi_f16_gemm's kernel takes run it; the rest run rocBLAS. */
 int madi_matmul_f16(const void *a, const void *b, void *c, int m, int n, int k, float alpha,
                     float beta);
 

@@ -1091,6 +1091,7 @@ NN_CASES = [
     (1500, 1280, 5120, O.EPI_NONE),       # fc2: 64 x 128, 80 chunks
     (65, 384, 192, O.EPI_BIAS_GELU),      # three chunks, 65 rows
     (1, 128, 64, O.EPI_BIAS),             # one row, one chunk
+    (24000, 5120, 1280, O.EPI_NONE),      # 16 windows: 3760 tiles, 15 rounds
 ]
 
 
@@ -1114,7 +1115,8 @@ def test_f16_nn_gemm(q, m, n, k, epi):
         q.kM4Bias("m4_gemm_bias_gelu" if epi == O.EPI_BIAS_GELU else "m4_gemm_bias",
                   dev_f16(a), dev_f16(b), dc, dev(bias), m, n, k)
     q.sync()
-    rows = np.unique(np.r_[0, 1, 31, 32, 63, 64, 127, 128, 255, 256, m // 2, m - 2, m - 1])
+    rows = np.unique(np.r_[0, 1, 31, 32, 63, 64, 127, 128, 255, 256, m // 2, m - 2, m - 1,
+                           np.arange(0, m, 1537)])
     rows = rows[(rows >= 0) & (rows < m)]
     got = host_f16(dc)[rows].astype(np.float64)
     c16 = O.gemm_f16(a[rows], b, threads=8)
