@@ -1134,6 +1134,44 @@ def test_f16_nn_gemm(q, m, n, k, epi):
     assert normwise(got, ref) <= TOL
 
 
+def test_f16_nn_gemm_random_shapes(q):
+    """Seeded random shapes the NN kernel takes (M any, N a multiple of 128,
+    K of 64), each epilogue in turn, element-wise against the oracle on every
+    row (fp32 accumulation + f16 rounding bound for the plain product,
+    normwise for the epilogues)."""
+    rng = np.random.default_rng(2024)
+    for t in range(8):
+        m = int(rng.integers(1, 400))
+        n = 128 * int(rng.integers(1, 17))
+        k = 64 * int(rng.integers(1, 25))
+        epi = (O.EPI_NONE, O.EPI_BIAS, O.EPI_BIAS_GELU)[t % 3]
+        say(f"f16 NN GEMM random m={m} n={n} k={k} epi={epi}")
+        a = rng.standard_normal((m, k)).astype(np.float16)
+        b = (rng.standard_normal((k, n)) * 0.05).astype(np.float16)
+        bias = rng.standard_normal(n).astype(np.float32)
+        dc = torch.full((m, n), -1, dtype=torch.int16, device="cuda")
+        if epi == O.EPI_NONE:
+            q.kM4("m4_gemm_nn", dev_f16(a), dev_f16(b), dc, m, n, k)
+        else:
+            q.kM4Bias("m4_gemm_bias_gelu" if epi == O.EPI_BIAS_GELU else "m4_gemm_bias",
+                      dev_f16(a), dev_f16(b), dc, dev(bias), m, n, k)
+        q.sync()
+        got = host_f16(dc).astype(np.float64)
+        c16 = O.gemm_f16(a, b, threads=8)
+        if epi == O.EPI_NONE:
+            exact = a.astype(np.float64) @ b.astype(np.float64)
+            bound = 2.0**-11 * np.abs(exact) + (k + 2) * 2.0**-24 * (
+                np.abs(a.astype(np.float64)) @ np.abs(b.astype(np.float64))) + 2.0**-24
+            assert np.all(np.abs(got - exact) <= bound * 1.001), (m, n, k)
+            ref = c16.astype(np.float64)
+        else:
+            v = c16.astype(np.float32) + bias[None, :]
+            if epi == O.EPI_BIAS_GELU:
+                v = np.vectorize(O.gelu_erf, otypes=[np.float32])(v)
+            ref = O.f32_to_f16(v).astype(np.float64)
+        assert normwise(got, ref) <= TOL, (m, n, k, epi)
+
+
 def test_f16_nn_gemm_leaves_other_rows(q):
     """Rows past M are never written (the last tile's clamped rows are read,
     not stored): the output sits inside a taller sentinel buffer."""
