@@ -231,7 +231,8 @@ int madi_q8_gemv_epi(int func, float *out, const float *x, const void *qs, const
  * . w16, w16 the F16 [K][N] copy deqW16 made of a Q8 weight.  A recorded
  * copy (below) runs madi_q8_pproj on the Q8 weight; a true F16 weight is
  * staged to f16 in stage16 ([B][K] f16, the BScratch in16 buffer) and
- * multiplied by a library GEMM with an f32 result. */
+ * multiplied by the NN f16 GEMM with an f32 result (rocBLAS for shapes it
+ * does not take). */
 int madi_proj_f16w(float *out, const float *in, const void *w16, void *stage16, uint32_t m,
                    uint32_t n, uint32_t k);
 

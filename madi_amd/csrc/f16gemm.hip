@@ -20,10 +20,11 @@
 // column c's 4 values), two per fragment.  The MFMA takes the B fragment as
 // its first operand, so each lane accumulates C^T (four consecutive columns
 // of one row); the finished tile goes through LDS and leaves as whole rows.
-// Shapes the kernel does not take (K not a multiple of 64, N not a multiple
-// of 128, misaligned rows), and matmulF16Batched with alpha != 1 or
-// beta != 0, run rocBLAS gemm_ex with fp32 accumulation; its bias epilogue
-// is then an elementwise pass.
+// proj (decoder.zig:337-341) on a true F16 weight stages its f32 rows to f16
+// and takes the same kernel with an f32 result.  Shapes the kernel does not
+// take (K not a multiple of 64, N not a multiple of 128, misaligned rows),
+// and matmulF16Batched with alpha != 1 or beta != 0, run rocBLAS gemm_ex with
+// fp32 accumulation; its bias epilogue is then an elementwise pass.
 #include <rocblas/rocblas.h>
 
 #include "common.h"
@@ -82,7 +83,8 @@ __device__ inline uint32_t swz_b(uint32_t row) { return (row & 3) << 2; }
 // XCD takes a contiguous run of tiles, column tiles outermost, and the B
 // columns of a run are fetched into one L2.  M rows past the last are read
 // as the last row (in bounds) and never stored.  Requires K % 64 == 0,
-// N % BN == 0, A, B, C and bias 16-byte aligned.
+// N % BN == 0, A, B, C and bias 16-byte aligned.  F32O: C is f32 (the
+// unrounded sums, no epilogue) instead of f16.
 //
 // Eight waves, two per SIMD: waves 0-3 compute (fragment reads and MFMAs),
 // waves 4-7 only issue the LDS DMAs.  A DMA waits for room in the address
@@ -92,11 +94,14 @@ __device__ inline uint32_t swz_b(uint32_t row) { return (row & 3) << 2; }
 // per chunk: the producers arrive once their DMAs of the chunk about to be
 // computed have landed (vmcnt), the computing waves once they are done
 // reading the chunk before, whose stage the producers refill right after.
-template <class G, int EPI>
+template <class G, int EPI, bool F32O>
 __global__ __launch_bounds__(512) void f16_nn_gemm_kernel(
     const f16 *__restrict__ A, const f16 *__restrict__ B, uint32_t M, uint32_t N, uint32_t K,
-    uint32_t tiles_m, uint32_t tiles, f16 *__restrict__ C, const float *__restrict__ bias) {
+    uint32_t tiles_m, uint32_t tiles, void *__restrict__ C, const float *__restrict__ bias) {
   constexpr int S = G::kStages, BN = G::BN, TMw = G::kTM, TNw = G::kTN, WNw = G::kWN;
+  static_assert(!F32O || EPI == MADI_EPI_NONE, "the f32 result takes no epilogue");
+  constexpr uint32_t kOut = F32O ? 4 : 2;  // bytes per C element
+  static_assert(G::BM * BN * kOut <= S * G::kStage, "the staged tile fits the ring");
   __shared__ __attribute__((aligned(1024))) uint8_t smem[S * G::kStage];
   const uint32_t lane = threadIdx.x & 63, wave8 = sgpr(threadIdx.x >> 6);
   const uint32_t wave = wave8 & 3;
@@ -109,7 +114,7 @@ __global__ __launch_bounds__(512) void f16_nn_gemm_kernel(
   const uint32_t tn = item / tiles_m, tm = item - tn * tiles_m;
   const uint32_t m0 = tm * G::BM, n0 = tn * BN, nk = K / 64;
   const uint32_t ring = lds_addr(smem);
-  constexpr uint32_t kPieces = BN / 8;  // 16-byte pieces per tile row
+  constexpr uint32_t kPieces = BN * kOut / 16;  // 16-byte pieces per tile row
 
   if (wave8 >= 4) {
     // ---- producer wave `wave`.  A: DMA j copies rows 8j .. 8j+7 of the
@@ -213,33 +218,39 @@ __global__ __launch_bounds__(512) void f16_nn_gemm_kernel(
     // GELU in registers, then the tile through LDS (free once every DMA has
     // landed and every fragment read is done), so that C leaves as whole rows
     // of 16-byte pieces; written straight from the MFMA layout, each store
-    // would touch 32 rows with 8 bytes.  Row t of the staged tile keeps its
-    // logical 16-byte piece p at p ^ (t & 15): the 8-byte writes of 32 rows
+    // would touch 32 rows with 8 (f32: 16) bytes.  Row t of the staged tile
+    // keeps its logical 16-byte piece p at p ^ (t & 15): the writes of 32 rows
     // at one piece, and the 16-byte reads of whole rows, spread over all banks.
     wait_then_barrier<0>();
 #pragma unroll
     for (int i = 0; i < TMw; ++i) {
       const uint32_t trow = 32 * TMw * wm + 32 * i + r;
-      const uint32_t rowb = ring + trow * (BN * 2), sw = trow & 15;
+      const uint32_t rowb = ring + trow * (BN * kOut), sw = trow & 15;
 #pragma unroll
       for (int j = 0; j < TNw; ++j) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           const uint32_t tcol = 32 * TNw * wn + 32 * j + 8 * q + 4 * h;
-          f16x4 o;
-          if constexpr (EPI == MADI_EPI_NONE) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = (f16)acc[i][j][4 * q + e];
+          if constexpr (F32O) {
+            const f32x4 o = {acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                             acc[i][j][4 * q + 3]};
+            *(lds_u32x4 *)(uintptr_t)(rowb + 16 * ((tcol >> 2) ^ sw)) = __builtin_bit_cast(u32x4, o);
           } else {
-            const f32x4 bv = *reinterpret_cast<const f32x4 *>(bias + n0 + tcol);
+            f16x4 o;
+            if constexpr (EPI == MADI_EPI_NONE) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              float v = (float)(f16)acc[i][j][4 * q + e] + bv[e];
-              if constexpr (EPI == MADI_EPI_BIAS_GELU) v = gelu_erf_fast(v);
-              o[e] = (f16)v;
+              for (int e = 0; e < 4; ++e) o[e] = (f16)acc[i][j][4 * q + e];
+            } else {
+              const f32x4 bv = *reinterpret_cast<const f32x4 *>(bias + n0 + tcol);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                float v = (float)(f16)acc[i][j][4 * q + e] + bv[e];
+                if constexpr (EPI == MADI_EPI_BIAS_GELU) v = gelu_erf_fast(v);
+                o[e] = (f16)v;
+              }
             }
+            *(lds_u32x2 *)(uintptr_t)(rowb + 16 * ((tcol >> 3) ^ sw) + 8 * h) = __builtin_bit_cast(u32x2, o);
           }
-          *(lds_u32x2 *)(uintptr_t)(rowb + 16 * ((tcol >> 3) ^ sw) + 8 * h) = __builtin_bit_cast(u32x2, o);
         }
       }
     }
@@ -250,8 +261,9 @@ __global__ __launch_bounds__(512) void f16_nn_gemm_kernel(
 #pragma unroll
   for (uint32_t s = 0; s < G::BM * kPieces / 512; ++s) {
     const uint32_t e = 512 * s + threadIdx.x, trow = e / kPieces, p = e % kPieces;
-    const u32x4 v = *(const lds_u32x4 *)(uintptr_t)(ring + trow * (BN * 2) + 16 * (p ^ (trow & 15)));
-    if (m0 + trow < M) *reinterpret_cast<u32x4 *>(C + (size_t)(m0 + trow) * N + n0 + 8 * p) = v;
+    const u32x4 v = *(const lds_u32x4 *)(uintptr_t)(ring + trow * (BN * kOut) + 16 * (p ^ (trow & 15)));
+    if (m0 + trow < M)
+      *reinterpret_cast<u32x4 *>(static_cast<uint8_t *>(C) + ((size_t)(m0 + trow) * N + n0) * kOut + 16 * p) = v;
   }
 }
 rocblas_handle g_blas = nullptr;
@@ -339,20 +351,23 @@ bool nn_ok(const void *a, const void *b, const void *c, const float *bias, uint3
          (uint64_t)k * n * 2 < (1ull << 31);
 }
 
-template <class G, int EPI>
+template <class G, int EPI, bool F32O = false>
 int launch_nn(const void *a, const void *b, void *c, const float *bias, uint32_t m, uint32_t n,
               uint32_t k, const char *what) {
   const uint32_t tiles_m = (m + G::BM - 1) / G::BM, tiles = tiles_m * (n / G::BN);
-  hipLaunchKernelGGL((f16_nn_gemm_kernel<G, EPI>), dim3((tiles + 7) & ~7u), dim3(512), 0, stream(),
-                     static_cast<const f16 *>(a), static_cast<const f16 *>(b), m, n, k, tiles_m,
-                     tiles, static_cast<f16 *>(c), bias);
+  hipLaunchKernelGGL((f16_nn_gemm_kernel<G, EPI, F32O>), dim3((tiles + 7) & ~7u), dim3(512), 0,
+                     stream(), static_cast<const f16 *>(a), static_cast<const f16 *>(b), m, n, k,
+                     tiles_m, tiles, c, bias);
   return check_launch(what);
 }
 
+// epi: an f16 result with that epilogue; kF32Out: the f32 result
+constexpr int kF32Out = -1;
 template <class G>
 int launch_nn_epi(int epi, const void *a, const void *b, void *c, const float *bias, uint32_t m,
                   uint32_t n, uint32_t k, const char *what) {
   switch (epi) {
+    case kF32Out: return launch_nn<G, MADI_EPI_NONE, true>(a, b, c, nullptr, m, n, k, what);
     case MADI_EPI_BIAS: return launch_nn<G, MADI_EPI_BIAS>(a, b, c, bias, m, n, k, what);
     case MADI_EPI_BIAS_GELU: return launch_nn<G, MADI_EPI_BIAS_GELU>(a, b, c, bias, m, n, k, what);
     default: return launch_nn<G, MADI_EPI_NONE>(a, b, c, nullptr, m, n, k, what);
@@ -476,5 +491,7 @@ extern "C" int madi_proj_f16w(float *out, const float *in, const void *w16, void
   hipLaunchKernelGGL(to_f16_kernel, dim3((unsigned)((count + 255) / 256)), dim3(256), 0, stream(),
                      static_cast<f16 *>(stage16), in, count);
   if (int rc = check_launch("madi_proj_f16w(stage)")) return rc;
+  if (nn_ok(stage16, w16, out, nullptr, m, n, k))
+    return nn_gemm(kF32Out, stage16, w16, out, nullptr, m, n, k, "madi_proj_f16w");
   return gemm_f16_f32out("madi_proj_f16w", stage16, w16, out, m, n, k);
 }

@@ -1172,6 +1172,30 @@ def test_f16_nn_gemm_random_shapes(q):
         assert normwise(got, ref) <= TOL, (m, n, k, epi)
 
 
+@pytest.mark.parametrize("m,n,k,shift", [(8, 5120, 1280, 0), (300, 1280, 1280, 0),
+                                         (1500, 5120, 1280, 0), (40, 1280, 1280, 1)])
+def test_proj_true_f16_weight(q, m, n, k, shift):
+    """proj (decoder.zig:337-341) on a true F16 weight: the activations
+    staged to f16 in the caller's in16 buffer, then the NN GEMM with an f32
+    result (an output 4 bytes off 16-byte alignment takes rocBLAS instead),
+    element-wise within fp32 accumulation of the exact f16 products."""
+    say(f"proj on a true F16 weight m={m} n={n} k={k} shift={shift}")
+    rng = np.random.default_rng(m + n + shift)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    w16 = (rng.standard_normal((k, n)) * 0.05).astype(np.float16)
+    in16 = torch.empty(m * k, dtype=torch.int16, device="cuda")
+    buf = torch.full((m * n + 4,), float("nan"), dtype=torch.float32, device="cuda")
+    out = buf[shift:shift + m * n]
+    q.proj(in16, dev(x), dev_f16(w16), out, m, n, k)
+    q.sync()
+    got = out.cpu().numpy().reshape(m, n).astype(np.float64)
+    a = x.astype(np.float16).astype(np.float64)
+    exact = a @ w16.astype(np.float64)
+    bound = (k + 2) * 2.0**-24 * (np.abs(a) @ np.abs(w16.astype(np.float64))) + 2.0**-30
+    assert np.all(np.abs(got - exact) <= bound)
+    assert np.array_equal(host_f16(in16).reshape(m, k), x.astype(np.float16))
+
+
 def test_f16_nn_gemm_leaves_other_rows(q):
     """Rows past M are never written (the last tile's clamped rows are read,
     not stored): the output sits inside a taller sentinel buffer."""
