@@ -76,6 +76,8 @@ __device__ inline f16x4 lds_read_tr(uint32_t addr) {
 // p ^ ((k & 3) << 2), so the eight rows of a transpose read (k, k+1, k+2,
 // k+3 and the same eight rows on) cover four distinct 64-byte bank groups twice.
 __device__ inline uint32_t swz_a(uint32_t row) { return (row >> 1) & 7; }
+// buffer cache policy sc1: a store writes through the XCD's L2
+constexpr int kSc1 = 16;
 __device__ inline uint32_t swz_b(uint32_t row) { return (row & 3) << 2; }
 
 // Grid: one workgroup per tile, the grid rounded up to a multiple of 8.
@@ -257,13 +259,19 @@ __global__ __launch_bounds__(512) void f16_nn_gemm_kernel(
     wait_then_barrier<0>();
   }
   // all eight waves store: thread t takes piece (512 s + t) of the tile in
-  // row-major order
+  // row-major order.  The stores write through the XCD's L2 (sc1): plain
+  // write-back stores would leave the whole of C as dirty lines for the
+  // release at the kernel's end to write back after the last workgroup.
+  // The resource spans the tile's rows that exist (rows past M fall outside).
+  const uint32_t rows = M - m0 < G::BM ? M - m0 : G::BM;
+  const __amdgpu_buffer_rsrc_t cr = __builtin_amdgcn_make_buffer_rsrc(
+      static_cast<uint8_t *>(C) + (size_t)m0 * N * kOut, 0, (int)(rows * N * kOut), 0x00020000);
 #pragma unroll
   for (uint32_t s = 0; s < G::BM * kPieces / 512; ++s) {
     const uint32_t e = 512 * s + threadIdx.x, trow = e / kPieces, p = e % kPieces;
     const u32x4 v = *(const lds_u32x4 *)(uintptr_t)(ring + trow * (BN * kOut) + 16 * (p ^ (trow & 15)));
-    if (m0 + trow < M)
-      *reinterpret_cast<u32x4 *>(static_cast<uint8_t *>(C) + ((size_t)(m0 + trow) * N + n0) * kOut + 16 * p) = v;
+    if (trow < rows)
+      __builtin_amdgcn_raw_buffer_store_b128(v, cr, (trow * N + n0) * kOut + 16 * p, 0, kSc1);
   }
 }
 rocblas_handle g_blas = nullptr;
@@ -343,12 +351,13 @@ __global__ __launch_bounds__(256) void bias_epilogue_kernel(f16 *__restrict__ c,
 }
 
 // Whether f16_nn_gemm_kernel takes the shape: K a multiple of 64, N of 128,
-// 16-byte aligned operands, A and B (its 32-bit buffer offsets) below 2 GiB.
+// 16-byte aligned operands, A, B and one 128-row tile of C (its 32-bit
+// buffer offsets) below 2 GiB.
 bool nn_ok(const void *a, const void *b, const void *c, const float *bias, uint32_t m, uint32_t n,
            uint32_t k) {
   return k % 64 == 0 && n % 128 == 0 && aligned(a, 16) && aligned(b, 16) && aligned(c, 16) &&
          (!bias || aligned(bias, 16)) && (uint64_t)m * k * 2 < (1ull << 31) &&
-         (uint64_t)k * n * 2 < (1ull << 31);
+         (uint64_t)k * n * 2 < (1ull << 31) && (uint64_t)n * 128 * 4 < (1ull << 31);
 }
 
 template <class G, int EPI, bool F32O = false>
